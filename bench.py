@@ -1,0 +1,225 @@
+"""Benchmark of the fused GGUF dequant-matmul on one MI355X.
+
+Headline (BASELINE.json metric "Q4_K decode GEMV HBM GB/s (% of peak)"):
+one step = one decode token's Q4_K projections at Llama-3-8B shapes, batch 1:
+W_gate-shape [14336 x 4096] and W_down-shape [4096 x 14336] (the two K-quant
+projection shapes of config 3), x fp16 N(0, 1), y fp32.  Weights are
+N(0, 0.02) quantised to Q4_K from a seed and replicated into a weight pool of
+>= 1 GiB of distinct device buffers that the steps rotate through, so every
+launch streams its weight from HBM, not from the 256 MB Infinity Cache.
+
+value = algorithmic bytes (GGUF-native weight bytes + x + y) per step x steps
+        / wall time of the timed steps (inputs resident in HBM).
+
+Also reported: the roofline of the dominant kernel (cq_gemv_q4_k_xf16_yf32)
+from per-launch HIP events, secondary numbers (lm_head Q6_K, batch 4/16,
+prefill TFLOP/s), and the reference CPU path (dequantise once, dense f32
+GEMV per call) timed on this host as cpu_baseline.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+
+
+def algo_bytes(wbytes, m, k, n, xbytes=2, ybytes=4):
+    return wbytes + m * k * xbytes + m * n * ybytes
+
+
+def make_pool(fmt, n, k, pool_bytes, seed):
+    import numpy as np
+    import torch
+    from combsengine_amd import QuantWeight, quantize
+    rng = np.random.default_rng(seed)
+    data = np.frombuffer(quantize(fmt, rng.normal(0, 0.02, (n, k)).astype(np.float32)), np.uint8)
+    base = torch.from_numpy(data.copy()).cuda()
+    count = max(1, int(pool_bytes // data.size))
+    pool = []
+    for i in range(count):
+        t = base if i == 0 else base.clone()
+        pool.append(QuantWeight.from_device(fmt, t, n, k))
+    return pool, data
+
+
+def time_launch_durations(fn, launches):
+    """Mean device duration of single launches, bracketed by HIP events on the
+    stream the kernel runs on (torch's current stream)."""
+    import torch
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(launches)]
+    for i, (a, b) in enumerate(evs):
+        a.record()
+        fn(i)
+        b.record()
+    torch.cuda.synchronize()
+    d = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)  # us
+    return sum(d) / len(d), d[len(d) // 10], d[len(d) // 2], d[(9 * len(d)) // 10]
+
+
+def cpu_baseline(seconds=6.0):
+    """Reference CPU path (dequantise at load, dense f32 GEMV per call) on the
+    headline gate shape, 1 thread (matrixmultiply without threading) and all
+    cores; reported in the same GB/s metric as the GPU."""
+    import numpy as np
+    import oracle as O
+    from combsengine_amd import QuantFormat, quantize
+    n, k = 14336, 4096
+    rng = np.random.default_rng(7)
+    data = np.frombuffer(quantize(QuantFormat.Q4K, rng.normal(0, 0.02, (n, k)).astype(np.float32)), np.uint8)
+    t0 = time.perf_counter()
+    w = O.dequant(O.Q4_K, data, n * k, threads=1).reshape(n, k)
+    t_deq = time.perf_counter() - t0
+    x = rng.normal(0, 1, (1, k)).astype(np.float16).astype(np.float32)
+    res = {}
+    for threads in (1, os.cpu_count() or 1):
+        calls, t0 = 0, time.perf_counter()
+        while True:
+            O.dense_gemm(x, w, threads)
+            calls += 1
+            el = time.perf_counter() - t0
+            if el > seconds / 2:
+                break
+        res[threads] = (calls, el)
+    per = algo_bytes(data.size, 1, k, n)
+    c1, e1 = res[1]
+    call_max = max(res)
+    cm, em = res[call_max]
+    return {
+        "value": round(per * c1 / e1 / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+        "sample": f"Q4_K [{n}x{k}] m=1: dequantise once ({t_deq:.2f} s, 1 thread), then {c1} dense f32 GEMV "
+                  f"calls in {e1:.1f} s on 1 thread (oracle restatement of llama.rs:81-97 -> sgemm)",
+        "all_cores": {"value": round(per * cm / em / 1e9, 3), "cores": call_max, "calls": cm},
+        "dequant_s": round(t_deq, 3), "ms_per_call_1t": round(e1 / c1 * 1e3, 3),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--pool-gib", type=float, default=1.25)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; the multi-GPU sharding is design-only "
+                          "(output-row split, see DESIGN.md)", "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    from combsengine_amd import QuantFormat
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    fmt = QuantFormat.Q4K
+    shapes = [(14336, 4096), (4096, 14336)]
+    pools, sizes = [], []
+    per_pool = args.pool_gib * (1 << 30) / len(shapes)
+    for si, (n, k) in enumerate(shapes):
+        p, data = make_pool(fmt, n, k, per_pool, seed=1000 + si)
+        pools.append(p)
+        sizes.append(data.size)
+    P = min(len(p) for p in pools)
+    rng = np.random.default_rng(5)
+    xs = [torch.from_numpy(rng.normal(0, 1, (1, k)).astype(np.float16)).to(dev) for (_, k) in shapes]
+    ys = [torch.empty((1, n), dtype=torch.float32, device=dev) for (n, _) in shapes]
+
+    def step(i):
+        e = i % P
+        for s in range(len(shapes)):
+            pools[s][e].matmul_into(xs[s], ys[s])
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for i in range(args.steps):
+        step(i)
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_total = ev0.elapsed_time(ev1)
+    step_bytes = sum(algo_bytes(sz, 1, k, n) for sz, (n, k) in zip(sizes, shapes))
+    value = step_bytes * args.steps / (ms_total / 1e3) / 1e9
+
+    # Dominant kernel: per-launch duration with HIP events, both shapes.
+    launch = {}
+    tot_b, tot_us = 0.0, 0.0
+    for s, (n, k) in enumerate(shapes):
+        mean, p10, p50, p90 = time_launch_durations(lambda i, s=s: pools[s][i % P].matmul_into(xs[s], ys[s]),
+                                                     max(4 * P, 200))
+        b = algo_bytes(sizes[s], 1, k, n)
+        launch[f"{n}x{k}"] = {"us_mean": round(mean, 3), "us_p10": round(p10, 3), "us_p50": round(p50, 3),
+                              "us_p90": round(p90, 3), "GBps": round(b / mean / 1e3, 1),
+                              "frac": round(b / mean / 1e3 / HBM_PEAK_GBS, 4)}
+        tot_b += b
+        tot_us += mean
+    achieved = tot_b / tot_us / 1e3
+
+    extra = {}
+    if not args.no_extra:
+        extra = secondary(dev)
+
+    line = {
+        "metric": "Q4_K decode GEMV HBM GB/s (% of peak); prefill dequant-GEMM TFLOP/s",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_total / args.steps, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "q4_k weights, f16 x, f32 accumulate/out", "data": "synthetic",
+        "config": {"workload": "Q4_K decode GEMV, Llama-3-8B shapes [14336x4096]+[4096x14336], batch 1, "
+                               f"weight pool {P} x {len(shapes)} buffers ({P * sum(sizes) / 2**30:.2f} GiB)",
+                   "global_batch": 1, "parallelism": "none (1 GPU)"},
+        "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "kernel": "cq_gemv_q4_k_xf16_yf32", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "algorithmic_bytes_per_launch": {f"{n}x{k}": algo_bytes(sz, 1, k, n)
+                                                                       for sz, (n, k) in zip(sizes, shapes)},
+                     "launches": launch},
+        "wall_s_timed": round(wall, 3),
+        "secondary": extra,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+def secondary(dev):
+    """lm_head Q6_K GEMV, batch 4/16 Q4_K, and prefill M=128/512 TFLOP/s."""
+    import numpy as np
+    import torch
+    from combsengine_amd import QuantFormat
+    out = {}
+    rng = np.random.default_rng(9)
+    # lm_head Q6_K [128256 x 4096] (431 MB: larger than the Infinity Cache)
+    pool, data = make_pool(QuantFormat.Q6K, 128256, 4096, 2 * 431e6, seed=77)
+    x = torch.from_numpy(rng.normal(0, 1, (1, 4096)).astype(np.float16)).to(dev)
+    y = torch.empty((1, 128256), dtype=torch.float32, device=dev)
+    mean, p10, p50, p90 = time_launch_durations(lambda i: pool[i % len(pool)].matmul_into(x, y), 40)
+    b = algo_bytes(data.size, 1, 4096, 128256)
+    out["lm_head_q6_k_m1"] = {"us": round(mean, 2), "GBps": round(b / mean / 1e3, 1)}
+    del pool
+    # batch 4 / 16 and prefill on the gate shape
+    pool, data = make_pool(QuantFormat.Q4K, 14336, 4096, 0.6 * (1 << 30), seed=1000)
+    for m in (4, 16, 128, 512):
+        x = torch.from_numpy(rng.normal(0, 1, (m, 4096)).astype(np.float16)).to(dev)
+        y = torch.empty((m, 14336), dtype=torch.float16 if m > 16 else torch.float32, device=dev)
+        reps = 40 if m <= 16 else 10
+        mean, p10, p50, p90 = time_launch_durations(lambda i: pool[i % len(pool)].matmul_into(x, y), reps)
+        b = algo_bytes(data.size, m, 4096, 14336, ybytes=2 if m > 16 else 4)
+        fl = 2.0 * m * 4096 * 14336
+        out[f"q4_k_14336x4096_m{m}"] = {"us": round(mean, 2), "GBps": round(b / mean / 1e3, 1),
+                                        "TFLOPs": round(fl / mean / 1e6, 2)}
+    return out
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,50 @@
+"""Build recipe for the gfx950 library (no cmake/ninja needed).
+
+1. hipcc --genco compiles csrc/cq_kernels.hip (all device code) into one
+   gfx950 code object, lib/cq_gfx950.hsaco.
+2. g++ compiles the host side (C ABI, module loading, quantisers) into
+   lib/libcombs_qlinear.so, embedding the code object with .incbin, and links
+   the HIP runtime (libamdhip64).
+
+The .so is self-contained: it loads its kernels with hipModuleLoadData at
+first use on each device.
+"""
+import os
+import subprocess
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+LIBDIR = os.path.join(HERE, "lib")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+HSACO = os.path.join(LIBDIR, "cq_gfx950.hsaco")
+SO = os.path.join(LIBDIR, "libcombs_qlinear.so")
+
+HIPCC_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17",
+               # packed fp32 ops off (the compiler must not emit v_pk_*_f32)
+               "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"build failed: {' '.join(cmd)}\n{err}")
+    if verbose and err.strip():
+        print(err)
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(LIBDIR, exist_ok=True)
+    _run([os.path.join(ROCM, "bin", "hipcc"), "--genco", *HIPCC_FLAGS,
+          os.path.join(CSRC, "cq_kernels.hip"), "-o", HSACO], verbose)
+    _run(["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-fopenmp", "-Wall",
+          "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", f'-DCQ_HSACO_PATH="{HSACO}"',
+          os.path.join(CSRC, "cq_host.cpp"), os.path.join(CSRC, "cq_quantize.cpp"),
+          f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-o", SO], verbose)
+    return SO
+
+
+if __name__ == "__main__":
+    build(verbose=True)

@@ -1,0 +1,427 @@
+// Decode GEMV over GGUF-packed weights on CDNA4 MFMA:  y[m, n] = sum_k x[m, k] * W[n, k]
+// for m <= 16 per launch tile.  Replaces the one-thread-per-output CubeCL
+// kernels q{4_0,5_0,8_0,4_k,5_k,6_k}_matmul_kernel
+// (engine/core/combs-models/src/qmatmul.rs:92-125, 386-423, 440-470, 881-930,
+// 1064-1117, 1184-1229).
+//
+// Work mapping.  A workgroup owns 16 weight rows and 16 activation rows and
+// splits the row's K range across its waves (unit u goes to wave u % nw).
+// Inside a wave, lane l owns weight row n0 + (l & 15) and k-group g = l >> 4;
+// each unit's packed bytes for that row are read by the 4 lanes of the row
+// with 16-byte loads, unpacked in registers to exact small-integer fp16
+// values (scale folded in where the product stays exact), and fed to
+// v_mfma_f32_16x16x32_f16 against the activations.  Per-block/superblock
+// scales (fp16 d, dmin) are applied to the fp32 MFMA result, so no weight is
+// ever rounded to fp16.
+//
+// Unpack trick: a 16-bit word 0x6400 | v is the fp16 number 1024 + v for
+// 0 <= v < 1024, so OR-ing nibbles under 0x6400 makes fp16 integers with no
+// conversion instruction; one v_pk_fma_f16 then removes the 1024 bias and
+// applies an integer scale exactly (single rounding of an exact integer).
+#pragma once
+#include "cq_common.h"
+
+struct GemvArgs {
+  const uint8_t* w;   // packed GGUF blocks, [N rows][row_bytes]
+  const void* x;      // [M][K] fp16 or fp32
+  void* y;            // [M][N] fp32 or fp16
+  long long row_bytes;
+  int M, N, K;
+  int units;          // work units per row
+};
+
+// Byte selectors for v_perm_b32(hi, lo, sel): byte i of the result takes
+// byte sel_i of {hi:lo}; 0x0c yields 0.
+#define SEL_B0_B1 0x0c010c00u   // [lo.b0, 0, lo.b1, 0]
+#define SEL_B2_B3 0x0c030c02u   // [lo.b2, 0, lo.b3, 0]
+#define SEL_X_B01 0x05010400u   // [lo.b0, hi.b0, lo.b1, hi.b1]
+#define SEL_X_B23 0x07030602u   // [lo.b2, hi.b2, lo.b3, hi.b3]
+
+// ---------------------------------------------------------------------------
+// Q4_K: 144-byte superblock [d f16][dmin f16][scales 12][qs 128]
+// (gguf.rs:894-925).  Lane group g takes qs[32g, 32g+32): its low nibbles are
+// sub-block 2g (k = 64g + 0..31), its high nibbles sub-block 2g+1
+// (k = 64g + 32..63).  MFMA step s (0..7) covers k = 64g + 8s + 0..7.
+// Main MFMA: B = q * sc (<= 15*63, exact).  Min MFMA: B = m (6-bit) so that
+// sum_k m(k) x_k = sum_sb m_sb * sum(x in sb).  y += d*Cmain - dmin*Cmin.
+struct FragQ4K {
+  u4v hdr, q0, q1;
+};
+__device__ __forceinline__ void load_q4k(FragQ4K& f, const uint8_t* sb, int g) {
+  f.hdr = ld_u128(sb);
+  f.q0 = ld_u128(sb + 16 + 32 * g);
+  f.q1 = ld_u128(sb + 32 + 32 * g);
+}
+template <int XT>
+__device__ __forceinline__ void compute_q4k(const FragQ4K& f, const XRow<XT>& xr, int k0, int g, f4& acc) {
+  uint32_t sc0, m0, sc1, m1;
+  scale_min_k4(2 * g, f.hdr.y, f.hdr.z, f.hdr.w, sc0, m0);
+  scale_min_k4(2 * g + 1, f.hdr.y, f.hdr.z, f.hdr.w, sc1, m1);
+  const h2 s_lo = hsplat((float)sc0), c_lo = hsplat(-1024.0f * (float)sc0);
+  const h2 s_hi = hsplat((float)sc1 * 0.0625f), c_hi = hsplat(-64.0f * (float)sc1);
+  const h2 mn0 = hsplat((float)m0), mn1 = hsplat((float)m1);
+  const uint32_t um0 = as_u32(mn0), um1 = as_u32(mn1);
+  const h8 bm0 = mk_h8(um0, um0, um0, um0), bm1 = mk_h8(um1, um1, um1, um1);
+  const uint32_t w[8] = {f.q0.x, f.q0.y, f.q0.z, f.q0.w, f.q1.x, f.q1.y, f.q1.z, f.q1.w};
+  f4 c = {0, 0, 0, 0}, cm = {0, 0, 0, 0};
+#pragma unroll
+  for (int s = 0; s < 8; s++) {
+    const uint32_t wa = w[2 * (s & 3)], wb = w[2 * (s & 3) + 1];
+    const uint32_t pa1 = perm(0, wa, SEL_B0_B1), pa2 = perm(0, wa, SEL_B2_B3);
+    const uint32_t pb1 = perm(0, wb, SEL_B0_B1), pb2 = perm(0, wb, SEL_B2_B3);
+    h8 b;
+    if (s < 4) {
+      b = mk_h8(pk_fma((pa1 & 0x000F000Fu) | 0x64006400u, s_lo, c_lo),
+                pk_fma((pa2 & 0x000F000Fu) | 0x64006400u, s_lo, c_lo),
+                pk_fma((pb1 & 0x000F000Fu) | 0x64006400u, s_lo, c_lo),
+                pk_fma((pb2 & 0x000F000Fu) | 0x64006400u, s_lo, c_lo));
+    } else {
+      b = mk_h8(pk_fma((pa1 & 0x00F000F0u) | 0x64006400u, s_hi, c_hi),
+                pk_fma((pa2 & 0x00F000F0u) | 0x64006400u, s_hi, c_hi),
+                pk_fma((pb1 & 0x00F000F0u) | 0x64006400u, s_hi, c_hi),
+                pk_fma((pb2 & 0x00F000F0u) | 0x64006400u, s_hi, c_hi));
+    }
+    const A8<XT> a = load_a8<XT>(xr, k0 + 64 * g + 8 * s);
+    c = mfma_x<XT>(a, b, c);
+    cm = mfma_x<XT>(a, s < 4 ? bm0 : bm1, cm);
+  }
+  const float d = f16_bits_to_f32(f.hdr.x), dmin = f16_bits_to_f32(f.hdr.x >> 16);
+#pragma unroll
+  for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(-dmin, cm[r], __builtin_fmaf(d, c[r], acc[r]));
+}
+
+// ---------------------------------------------------------------------------
+// Q5_K: 176-byte superblock [d][dmin][scales 12][qh 32][qs 128]
+// (gguf.rs:929-961).  As Q4_K; the 5th bit of value (pair j, byte l, half t)
+// is bit 2j+t of qh[l].  Lane group g is pair j = g.
+struct FragQ5K {
+  u4v hdr, h0, h1, q0, q1;
+};
+__device__ __forceinline__ void load_q5k(FragQ5K& f, const uint8_t* sb, int g) {
+  f.hdr = ld_u128(sb);
+  f.h0 = ld_u128(sb + 16);
+  f.h1 = ld_u128(sb + 32);
+  f.q0 = ld_u128(sb + 48 + 32 * g);
+  f.q1 = ld_u128(sb + 64 + 32 * g);
+}
+template <int XT>
+__device__ __forceinline__ void compute_q5k(const FragQ5K& f, const XRow<XT>& xr, int k0, int g, f4& acc) {
+  uint32_t sc0, m0, sc1, m1;
+  scale_min_k4(2 * g, f.hdr.y, f.hdr.z, f.hdr.w, sc0, m0);
+  scale_min_k4(2 * g + 1, f.hdr.y, f.hdr.z, f.hdr.w, sc1, m1);
+  const h2 s_lo = hsplat((float)sc0), c_lo = hsplat(-1024.0f * (float)sc0);
+  const h2 s_hi = hsplat((float)sc1 * 0.0625f), c_hi = hsplat(-64.0f * (float)sc1);
+  const uint32_t um0 = as_u32(hsplat((float)m0)), um1 = as_u32(hsplat((float)m1));
+  const h8 bm0 = mk_h8(um0, um0, um0, um0), bm1 = mk_h8(um1, um1, um1, um1);
+  const uint32_t w[8] = {f.q0.x, f.q0.y, f.q0.z, f.q0.w, f.q1.x, f.q1.y, f.q1.z, f.q1.w};
+  const uint32_t hb[8] = {f.h0.x, f.h0.y, f.h0.z, f.h0.w, f.h1.x, f.h1.y, f.h1.z, f.h1.w};
+  const int shl = 2 * g, shh = 2 * g + 1;
+  f4 c = {0, 0, 0, 0}, cm = {0, 0, 0, 0};
+#pragma unroll
+  for (int s = 0; s < 8; s++) {
+    const int i0 = 2 * (s & 3);
+    uint32_t u[4];
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      const uint32_t wq = w[i0 + e], hq = hb[i0 + e];
+      if (s < 4) {
+        // bit 2g of each qh byte -> bit 4 of the byte, merged under the low nibble.
+        const uint32_t z = (wq & 0x0F0F0F0Fu) | (((hq >> shl) << 4) & 0x10101010u);
+        u[2 * e] = pk_fma((perm(0, z, SEL_B0_B1) & 0x001F001Fu) | 0x64006400u, s_lo, c_lo);
+        u[2 * e + 1] = pk_fma((perm(0, z, SEL_B2_B3) & 0x001F001Fu) | 0x64006400u, s_lo, c_lo);
+      } else {
+        // high nibble at bits 4-7 of the half, bit 2g+1 of qh at bit 8.
+        const uint32_t hx = hq >> shh;
+        u[2 * e] = pk_fma((perm(hx, wq, SEL_X_B01) & 0x01F001F0u) | 0x64006400u, s_hi, c_hi);
+        u[2 * e + 1] = pk_fma((perm(hx, wq, SEL_X_B23) & 0x01F001F0u) | 0x64006400u, s_hi, c_hi);
+      }
+    }
+    const h8 b = mk_h8(u[0], u[1], u[2], u[3]);
+    const A8<XT> a = load_a8<XT>(xr, k0 + 64 * g + 8 * s);
+    c = mfma_x<XT>(a, b, c);
+    cm = mfma_x<XT>(a, s < 4 ? bm0 : bm1, cm);
+  }
+  const float d = f16_bits_to_f32(f.hdr.x), dmin = f16_bits_to_f32(f.hdr.x >> 16);
+#pragma unroll
+  for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(-dmin, cm[r], __builtin_fmaf(d, c[r], acc[r]));
+}
+
+// ---------------------------------------------------------------------------
+// Q6_K: 210-byte superblock [ql 128][qh 64][scales 16 x i8][d f16]
+// (gguf.rs:968-999).  Value (half hh, quadrant t, l) = (ql nibble | 2 qh bits
+// << 4) - 32 with scale sc[8hh + l/16 + 2t].  Lane group g = (hh = g>>1,
+// s = g&1) owns l in [16s, 16s+16) for all four quadrants of half hh.
+// The i8 scale is split sc = 16*sh + sl (sh in [-8,7], sl in [0,15]) so both
+// (q-32)*sh and (q-32)*sl are exact in fp16; y += d * (16*Chi + Clo).
+struct FragQ6K {
+  u4v qa, qb, qh;
+  u2v sc;
+  uint32_t d;
+};
+__device__ __forceinline__ void load_q6k(FragQ6K& f, const uint8_t* sb, int g) {
+  const int hh = g >> 1, s = g & 1;
+  f.qa = ld_u128(sb + 64 * hh + 16 * s);
+  f.qb = ld_u128(sb + 64 * hh + 32 + 16 * s);
+  f.qh = ld_u128(sb + 128 + 32 * hh + 16 * s);
+  f.sc = ld_u64(sb + 192 + 8 * hh);
+  f.d = ld_u16(sb + 208);
+}
+template <int XT>
+__device__ __forceinline__ void compute_q6k(const FragQ6K& f, const XRow<XT>& xr, int k0, int g, f4& acc) {
+  const int hh = g >> 1, s = g & 1;
+  const uint32_t qa[4] = {f.qa.x, f.qa.y, f.qa.z, f.qa.w};
+  const uint32_t qb[4] = {f.qb.x, f.qb.y, f.qb.z, f.qb.w};
+  const uint32_t qh[4] = {f.qh.x, f.qh.y, f.qh.z, f.qh.w};
+  f4 chi = {0, 0, 0, 0}, clo = {0, 0, 0, 0};
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    // scale byte index s + 2t within the 8 scales of this half
+    const uint32_t word = (t < 2) ? f.sc.x : f.sc.y;
+    const int sc = (int)(int8_t)((word >> (8 * ((s + 2 * t) & 3))) & 0xFF);
+    const int shv = sc >> 4, slv = sc & 15;
+    h2 sh_s, sh_c, sl_s, sl_c;
+    if (t < 2) {  // value = 1024 + q6
+      sh_s = hsplat((float)shv); sh_c = hsplat(-1056.0f * (float)shv);
+      sl_s = hsplat((float)slv); sl_c = hsplat(-1056.0f * (float)slv);
+    } else {      // value = 1024 + 16*q6
+      sh_s = hsplat((float)shv * 0.0625f); sh_c = hsplat(-96.0f * (float)shv);
+      sl_s = hsplat((float)slv * 0.0625f); sl_c = hsplat(-96.0f * (float)slv);
+    }
+    const uint32_t* ql = (t & 1) ? qb : qa;
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      uint32_t uh[4], ul[4];
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        const uint32_t wq = ql[2 * e + i], hq = qh[2 * e + i];
+        uint32_t v1, v2;
+        if (t < 2) {
+          // qh bits 2t,2t+1 -> bits 4,5 of each byte, under the low nibble
+          const uint32_t z = (wq & 0x0F0F0F0Fu) | ((hq << (4 - 2 * t)) & 0x30303030u);
+          v1 = (perm(0, z, SEL_B0_B1) & 0x003F003Fu) | 0x64006400u;
+          v2 = (perm(0, z, SEL_B2_B3) & 0x003F003Fu) | 0x64006400u;
+        } else {
+          // high nibble at bits 4-7, qh bits 2t,2t+1 at bits 8,9
+          const uint32_t hx = hq >> (2 * t);
+          v1 = (perm(hx, wq, SEL_X_B01) & 0x03F003F0u) | 0x64006400u;
+          v2 = (perm(hx, wq, SEL_X_B23) & 0x03F003F0u) | 0x64006400u;
+        }
+        uh[2 * i] = pk_fma(v1, sh_s, sh_c);
+        uh[2 * i + 1] = pk_fma(v2, sh_s, sh_c);
+        ul[2 * i] = pk_fma(v1, sl_s, sl_c);
+        ul[2 * i + 1] = pk_fma(v2, sl_s, sl_c);
+      }
+      const A8<XT> a = load_a8<XT>(xr, k0 + 128 * hh + 32 * t + 16 * s + 8 * e);
+      chi = mfma_x<XT>(a, mk_h8(uh[0], uh[1], uh[2], uh[3]), chi);
+      clo = mfma_x<XT>(a, mk_h8(ul[0], ul[1], ul[2], ul[3]), clo);
+    }
+  }
+  const float d = f16_bits_to_f32(f.d);
+#pragma unroll
+  for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(d, __builtin_fmaf(16.0f, chi[r], clo[r]), acc[r]);
+}
+
+// ---------------------------------------------------------------------------
+// 32-value legacy blocks.  A unit is LB consecutive blocks of one row; every
+// block is one MFMA step with its own fp16 scale, applied to the fp32 result.
+#define LB 4
+
+// Q4_0: 18-byte block [d][qs 16] (gguf.rs:755-774).  Lane group g takes
+// qs[4g, 4g+4): low nibbles are k = 4g..4g+3, high nibbles k = 16+4g..16+4g+3.
+struct FragQ40 {
+  uint32_t q[LB], d[LB];
+};
+__device__ __forceinline__ void load_q40(FragQ40& f, const uint8_t* b, int g, int nb) {
+#pragma unroll
+  for (int i = 0; i < LB; i++) {
+    const int ii = i < nb ? i : 0;
+    f.q[i] = ld_u32(b + 18 * ii + 2 + 4 * g);
+    f.d[i] = ld_u16(b + 18 * ii);
+  }
+}
+template <int XT>
+__device__ __forceinline__ void compute_q40(const FragQ40& f, const XRow<XT>& xr, int k0, int g, int nb, f4& acc) {
+  const h2 one = hsplat(1.0f), c_lo = hsplat(-1032.0f);
+  const h2 s16 = hsplat(0.0625f), c_hi = hsplat(-72.0f);
+#pragma unroll
+  for (int i = 0; i < LB; i++) {
+    if (i >= nb) break;
+    const uint32_t p1 = perm(0, f.q[i], SEL_B0_B1), p2 = perm(0, f.q[i], SEL_B2_B3);
+    const h8 b = mk_h8(pk_fma((p1 & 0x000F000Fu) | 0x64006400u, one, c_lo),
+                       pk_fma((p2 & 0x000F000Fu) | 0x64006400u, one, c_lo),
+                       pk_fma((p1 & 0x00F000F0u) | 0x64006400u, s16, c_hi),
+                       pk_fma((p2 & 0x00F000F0u) | 0x64006400u, s16, c_hi));
+    const int kb = k0 + 32 * i;
+    const A8<XT> a = load_a4x2<XT>(xr, kb + 4 * g, kb + 16 + 4 * g);
+    const f4 c = mfma_x<XT>(a, b, f4{0, 0, 0, 0});
+    const float d = f16_bits_to_f32(f.d[i]);
+#pragma unroll
+    for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(d, c[r], acc[r]);
+  }
+}
+
+// Q5_0: 22-byte block [d][qh u32][qs 16] (gguf.rs:825-847).  Same k mapping
+// as Q4_0; value j's 5th bit is qh bit j (low nibbles) or j+16 (high).
+struct FragQ50 {
+  uint32_t q[LB], h[LB], d[LB];
+};
+__device__ __forceinline__ void load_q50(FragQ50& f, const uint8_t* b, int g, int nb) {
+#pragma unroll
+  for (int i = 0; i < LB; i++) {
+    const int ii = i < nb ? i : 0;
+    f.d[i] = ld_u16(b + 22 * ii);
+    f.h[i] = ld_u32(b + 22 * ii + 2);
+    f.q[i] = ld_u32(b + 22 * ii + 6 + 4 * g);
+  }
+}
+// bits 0..3 of v -> bit 0 of bytes 0..3 (no carries: all partial products
+// land on distinct bit positions).
+__device__ __forceinline__ uint32_t spread4(uint32_t v) {
+  return ((v & 0xFu) * 0x00204081u) & 0x01010101u;
+}
+template <int XT>
+__device__ __forceinline__ void compute_q50(const FragQ50& f, const XRow<XT>& xr, int k0, int g, int nb, f4& acc) {
+  const h2 one = hsplat(1.0f), c_lo = hsplat(-1040.0f);
+  const h2 s16 = hsplat(0.0625f), c_hi = hsplat(-80.0f);
+#pragma unroll
+  for (int i = 0; i < LB; i++) {
+    if (i >= nb) break;
+    const uint32_t q = f.q[i];
+    const uint32_t hl = spread4(f.h[i] >> (4 * g));
+    const uint32_t hh = spread4(f.h[i] >> (16 + 4 * g));
+    const uint32_t z = (q & 0x0F0F0F0Fu) | (hl << 4);
+    const h8 b = mk_h8(pk_fma((perm(0, z, SEL_B0_B1) & 0x001F001Fu) | 0x64006400u, one, c_lo),
+                       pk_fma((perm(0, z, SEL_B2_B3) & 0x001F001Fu) | 0x64006400u, one, c_lo),
+                       pk_fma((perm(hh, q, SEL_X_B01) & 0x01F001F0u) | 0x64006400u, s16, c_hi),
+                       pk_fma((perm(hh, q, SEL_X_B23) & 0x01F001F0u) | 0x64006400u, s16, c_hi));
+    const int kb = k0 + 32 * i;
+    const A8<XT> a = load_a4x2<XT>(xr, kb + 4 * g, kb + 16 + 4 * g);
+    const f4 c = mfma_x<XT>(a, b, f4{0, 0, 0, 0});
+    const float d = f16_bits_to_f32(f.d[i]);
+#pragma unroll
+    for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(d, c[r], acc[r]);
+  }
+}
+
+// Q8_0: 34-byte block [d][qs 32 x i8] (gguf.rs:779-794).  Lane group g takes
+// qs[8g, 8g+8) = k 8g..8g+7.  i8 s -> fp16 via (s ^ 0x80) = s + 128 placed
+// under a 0x64 high byte: 1024 + s + 128, minus 1152.
+struct FragQ80 {
+  u2v q[LB];
+  uint32_t d[LB];
+};
+__device__ __forceinline__ void load_q80(FragQ80& f, const uint8_t* b, int g, int nb) {
+#pragma unroll
+  for (int i = 0; i < LB; i++) {
+    const int ii = i < nb ? i : 0;
+    f.d[i] = ld_u16(b + 34 * ii);
+    f.q[i] = ld_u64(b + 34 * ii + 2 + 8 * g);
+  }
+}
+template <int XT>
+__device__ __forceinline__ void compute_q80(const FragQ80& f, const XRow<XT>& xr, int k0, int g, int nb, f4& acc) {
+  const h2 one = hsplat(1.0f), cb = hsplat(-1152.0f);
+#pragma unroll
+  for (int i = 0; i < LB; i++) {
+    if (i >= nb) break;
+    const uint32_t x0 = f.q[i].x ^ 0x80808080u, x1 = f.q[i].y ^ 0x80808080u;
+    const h8 b = mk_h8(pk_fma(perm(0x64646464u, x0, 0x04010400u), one, cb),
+                       pk_fma(perm(0x64646464u, x0, 0x04030402u), one, cb),
+                       pk_fma(perm(0x64646464u, x1, 0x04010400u), one, cb),
+                       pk_fma(perm(0x64646464u, x1, 0x04030402u), one, cb));
+    const A8<XT> a = load_a8<XT>(xr, k0 + 32 * i + 8 * g);
+    const f4 c = mfma_x<XT>(a, b, f4{0, 0, 0, 0});
+    const float d = f16_bits_to_f32(f.d[i]);
+#pragma unroll
+    for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(d, c[r], acc[r]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+template <int FMT> struct FmtTraits;
+template <> struct FmtTraits<CQ_Q4_K> { static constexpr int vals = 256, bytes = 144; typedef FragQ4K Frag; };
+template <> struct FmtTraits<CQ_Q5_K> { static constexpr int vals = 256, bytes = 176; typedef FragQ5K Frag; };
+template <> struct FmtTraits<CQ_Q6_K> { static constexpr int vals = 256, bytes = 210; typedef FragQ6K Frag; };
+template <> struct FmtTraits<CQ_Q4_0> { static constexpr int vals = 32 * LB, bytes = 18 * LB; typedef FragQ40 Frag; };
+template <> struct FmtTraits<CQ_Q5_0> { static constexpr int vals = 32 * LB, bytes = 22 * LB; typedef FragQ50 Frag; };
+template <> struct FmtTraits<CQ_Q8_0> { static constexpr int vals = 32 * LB, bytes = 34 * LB; typedef FragQ80 Frag; };
+
+template <int FMT>
+__device__ __forceinline__ void load_unit(typename FmtTraits<FMT>::Frag& f, const uint8_t* p, int g, int nb) {
+  if constexpr (FMT == CQ_Q4_K) load_q4k(f, p, g);
+  else if constexpr (FMT == CQ_Q5_K) load_q5k(f, p, g);
+  else if constexpr (FMT == CQ_Q6_K) load_q6k(f, p, g);
+  else if constexpr (FMT == CQ_Q4_0) load_q40(f, p, g, nb);
+  else if constexpr (FMT == CQ_Q5_0) load_q50(f, p, g, nb);
+  else load_q80(f, p, g, nb);
+}
+
+template <int FMT, int XT>
+__device__ __forceinline__ void compute_unit(const typename FmtTraits<FMT>::Frag& f, const XRow<XT>& xr, int k0,
+                                             int g, int nb, f4& acc) {
+  if constexpr (FMT == CQ_Q4_K) compute_q4k<XT>(f, xr, k0, g, acc);
+  else if constexpr (FMT == CQ_Q5_K) compute_q5k<XT>(f, xr, k0, g, acc);
+  else if constexpr (FMT == CQ_Q6_K) compute_q6k<XT>(f, xr, k0, g, acc);
+  else if constexpr (FMT == CQ_Q4_0) compute_q40<XT>(f, xr, k0, g, nb, acc);
+  else if constexpr (FMT == CQ_Q5_0) compute_q50<XT>(f, xr, k0, g, nb, acc);
+  else compute_q80<XT>(f, xr, k0, g, nb, acc);
+}
+
+#define CQ_MAX_WAVES 16
+
+// Grid: x = ceil(N/16) row tiles, y = ceil(M/16) activation tiles.
+// Block: 64 * nw threads, nw in 1..16.
+template <int FMT, int XT, int YT>
+__device__ __forceinline__ void gemv_body(const GemvArgs& a) {
+  typedef FmtTraits<FMT> T;
+  __shared__ float red[CQ_MAX_WAVES][4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int j = lane & 15, g = lane >> 4;
+  const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 16;
+  const int row = min(n0 + j, a.N - 1);
+  const uint8_t* wr = a.w + (size_t)row * a.row_bytes;
+  const XRow<XT> xr(a.x, m0 + j, a.M, a.K);
+  // legacy formats: blocks in the last (ragged) unit of the row
+  const int blocks = a.K / 32;
+  f4 acc = {0, 0, 0, 0};
+  typename T::Frag cur, nxt;
+  int u = wave;
+  if (u < a.units) {
+    const int nb = (T::vals == 256) ? 0 : min(LB, blocks - u * LB);
+    load_unit<FMT>(cur, wr + (size_t)u * T::bytes, g, nb);
+  }
+  for (; u < a.units; u += nw) {
+    const int nb = (T::vals == 256) ? 0 : min(LB, blocks - u * LB);
+    const int un = u + nw;
+    if (un < a.units) {
+      const int nbn = (T::vals == 256) ? 0 : min(LB, blocks - un * LB);
+      load_unit<FMT>(nxt, wr + (size_t)un * T::bytes, g, nbn);
+    }
+    compute_unit<FMT, XT>(cur, xr, u * T::vals, g, nb, acc);
+    cur = nxt;
+  }
+  if (nw > 1) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) red[wave][r][lane] = acc[r];
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < 256; idx += blockDim.x) {
+      const int r = idx >> 6, ln = idx & 63;
+      float s = red[0][r][ln];
+      for (int w2 = 1; w2 < nw; w2++) s += red[w2][r][ln];
+      const int m = m0 + 4 * (ln >> 4) + r, n = n0 + (ln & 15);
+      if (m < a.M && n < a.N) {
+        if (YT) ((_Float16*)a.y)[(size_t)m * a.N + n] = (_Float16)s;
+        else ((float*)a.y)[(size_t)m * a.N + n] = s;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int m = m0 + 4 * g + r, n = n0 + j;
+      if (m < a.M && n < a.N) {
+        if (YT) ((_Float16*)a.y)[(size_t)m * a.N + n] = (_Float16)acc[r];
+        else ((float*)a.y)[(size_t)m * a.N + n] = acc[r];
+      }
+    }
+  }
+}

@@ -1,0 +1,350 @@
+// Host side of the C ABI declared in include/combs_qlinear.h.
+//
+// The gfx950 code object built from cq_kernels.hip is embedded in this
+// library (.incbin) and loaded per device with hipModuleLoadData; kernels are
+// launched with hipModuleLaunchKernel.  Everything here is validation,
+// launch geometry and error reporting: there is no host compute path.
+#include <hip/hip_runtime_api.h>
+
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <mutex>
+#include <string>
+
+#include "../../include/combs_qlinear.h"
+
+#ifndef CQ_HSACO_PATH
+#error "CQ_HSACO_PATH must name the gfx950 code object to embed"
+#endif
+
+__asm__(".section .rodata\n"
+        ".global cq_hsaco_image\n"
+        ".balign 4096\n"
+        "cq_hsaco_image:\n"
+        ".incbin \"" CQ_HSACO_PATH "\"\n"
+        ".global cq_hsaco_image_end\n"
+        "cq_hsaco_image_end:\n"
+        ".byte 0\n"
+        ".previous\n");
+extern "C" const unsigned char cq_hsaco_image[];
+extern "C" const unsigned char cq_hsaco_image_end[];
+
+namespace {
+
+thread_local std::string g_err;
+
+cq_status fail(cq_status st, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return st;
+}
+
+#define HIP_TRY(call)                                                                        \
+  do {                                                                                       \
+    hipError_t e_ = (call);                                                                  \
+    if (e_ != hipSuccess) return fail(CQ_ERR_HIP, "%s: %s", #call, hipGetErrorString(e_));   \
+  } while (0)
+
+int block_values(int f) {
+  switch (f) {
+    case CQ_Q4_0: case CQ_Q5_0: case CQ_Q8_0: return 32;
+    case CQ_Q4_K: case CQ_Q5_K: case CQ_Q6_K: return 256;
+    default: return 0;
+  }
+}
+int block_bytes(int f) {
+  switch (f) {
+    case CQ_Q4_0: return 18;
+    case CQ_Q5_0: return 22;
+    case CQ_Q8_0: return 34;
+    case CQ_Q4_K: return 144;
+    case CQ_Q5_K: return 176;
+    case CQ_Q6_K: return 210;
+    default: return 0;
+  }
+}
+const char* fmt_name(int f) {
+  switch (f) {
+    case CQ_Q4_0: return "q4_0";
+    case CQ_Q5_0: return "q5_0";
+    case CQ_Q8_0: return "q8_0";
+    case CQ_Q4_K: return "q4_k";
+    case CQ_Q5_K: return "q5_k";
+    case CQ_Q6_K: return "q6_k";
+    default: return nullptr;
+  }
+}
+int fmt_index(int f) {
+  switch (f) {
+    case CQ_Q4_0: return 0;
+    case CQ_Q5_0: return 1;
+    case CQ_Q8_0: return 2;
+    case CQ_Q4_K: return 3;
+    case CQ_Q5_K: return 4;
+    case CQ_Q6_K: return 5;
+    default: return -1;
+  }
+}
+const int kFormats[6] = {CQ_Q4_0, CQ_Q5_0, CQ_Q8_0, CQ_Q4_K, CQ_Q5_K, CQ_Q6_K};
+
+// Kernel argument blocks; layouts match GemvArgs / DequantArgs in the .h files
+// compiled into the code object.
+struct GemvArgs {
+  const void* w;
+  const void* x;
+  void* y;
+  long long row_bytes;
+  int M, N, K;
+  int units;
+};
+struct DequantArgs {
+  const void* w;
+  float* out;
+  long long chunks;
+};
+
+constexpr int kMaxDevices = 64;
+
+struct DeviceModule {
+  std::once_flag once;
+  cq_status status = CQ_ERR_NO_DEVICE;
+  std::string err;
+  hipModule_t mod = nullptr;
+  hipFunction_t gemv[6][2][2] = {};  // [format][x f32][y f16]
+  hipFunction_t dequant[6] = {};
+};
+DeviceModule g_dev[kMaxDevices];
+
+void load_module(DeviceModule& d, int dev) {
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+    d.err = "hipGetDeviceProperties failed";
+    return;
+  }
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    d.err = std::string("device is ") + prop.gcnArchName + ", this library is built for gfx950 only";
+    return;
+  }
+  hipError_t e = hipModuleLoadData(&d.mod, cq_hsaco_image);
+  if (e != hipSuccess) {
+    d.err = std::string("hipModuleLoadData: ") + hipGetErrorString(e);
+    return;
+  }
+  char name[96];
+  for (int fi = 0; fi < 6; fi++) {
+    const char* fn = fmt_name(kFormats[fi]);
+    for (int xt = 0; xt < 2; xt++)
+      for (int yt = 0; yt < 2; yt++) {
+        snprintf(name, sizeof name, "cq_gemv_%s_x%s_y%s", fn, xt ? "f32" : "f16", yt ? "f16" : "f32");
+        if (hipModuleGetFunction(&d.gemv[fi][xt][yt], d.mod, name) != hipSuccess) {
+          d.err = std::string("missing kernel ") + name;
+          return;
+        }
+      }
+    snprintf(name, sizeof name, "cq_dequant_%s", fn);
+    if (hipModuleGetFunction(&d.dequant[fi], d.mod, name) != hipSuccess) {
+      d.err = std::string("missing kernel ") + name;
+      return;
+    }
+  }
+  d.status = CQ_OK;
+}
+
+cq_status device_module(DeviceModule** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(CQ_ERR_NO_DEVICE, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(CQ_ERR_NO_DEVICE, "device id %d out of range", dev);
+  DeviceModule& d = g_dev[dev];
+  std::call_once(d.once, load_module, std::ref(d), dev);
+  if (d.status != CQ_OK) return fail(d.status, "device %d: %s", dev, d.err.c_str());
+  *out = &d;
+  return CQ_OK;
+}
+
+int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return (v && *v) ? atoi(v) : dflt;
+}
+
+}  // namespace
+
+struct cq_weight {
+  int format;
+  int64_t n, k;
+  size_t nbytes;
+  void* dev;
+  bool owned;
+  int device;
+};
+
+extern "C" {
+
+int cq_block_values(int format) { return block_values(format); }
+int cq_block_bytes(int format) { return block_bytes(format); }
+
+cq_status cq_tensor_bytes(int format, int64_t n, int64_t k, size_t* out_bytes) {
+  const int qk = block_values(format);
+  if (!qk) return fail(CQ_ERR_BAD_FORMAT, "unsupported format id %d", format);
+  if (!out_bytes) return fail(CQ_ERR_NULL, "out_bytes is NULL");
+  if (n < 1 || k < 1 || k % qk != 0)
+    return fail(CQ_ERR_BAD_SHAPE, "[n=%lld, k=%lld]: k must be a positive multiple of %d", (long long)n,
+                (long long)k, qk);
+  *out_bytes = (size_t)n * (size_t)(k / qk) * (size_t)block_bytes(format);
+  return CQ_OK;
+}
+
+static cq_status validate(int format, const void* bytes, size_t nbytes, int64_t n, int64_t k, cq_weight** out) {
+  if (!out) return fail(CQ_ERR_NULL, "out is NULL");
+  *out = nullptr;
+  if (!bytes) return fail(CQ_ERR_NULL, "weight bytes pointer is NULL");
+  size_t expect = 0;
+  cq_status st = cq_tensor_bytes(format, n, k, &expect);
+  if (st != CQ_OK) return st;
+  if (nbytes != expect)
+    return fail(CQ_ERR_BAD_SHAPE, "%s weight [%lld, %lld] needs %zu bytes, got %zu", fmt_name(format),
+                (long long)n, (long long)k, expect, nbytes);
+  if (k / block_values(format) > (int64_t)0x7fffffff || n > (int64_t)0x7fffffff)
+    return fail(CQ_ERR_BAD_SHAPE, "dimension too large");
+  return CQ_OK;
+}
+
+cq_status cq_weight_create(int format, const void* host_bytes, size_t nbytes, int64_t n, int64_t k, void* stream,
+                           cq_weight** out) {
+  cq_status st = validate(format, host_bytes, nbytes, n, k, out);
+  if (st != CQ_OK) return st;
+  DeviceModule* dm;
+  if ((st = device_module(&dm)) != CQ_OK) return st;
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  void* p = nullptr;
+  HIP_TRY(hipMalloc(&p, nbytes));
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = hipMemcpyAsync(p, host_bytes, nbytes, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) {
+    (void)hipFree(p);
+    return fail(CQ_ERR_HIP, "weight upload: %s", hipGetErrorString(e));
+  }
+  *out = new cq_weight{format, n, k, nbytes, p, true, dev};
+  return CQ_OK;
+}
+
+cq_status cq_weight_wrap_device(int format, const void* device_bytes, size_t nbytes, int64_t n, int64_t k,
+                                cq_weight** out) {
+  cq_status st = validate(format, device_bytes, nbytes, n, k, out);
+  if (st != CQ_OK) return st;
+  int dev = 0;
+  HIP_TRY(hipGetDevice(&dev));
+  *out = new cq_weight{format, n, k, nbytes, const_cast<void*>(device_bytes), false, dev};
+  return CQ_OK;
+}
+
+void cq_weight_destroy(cq_weight* w) {
+  if (!w) return;
+  if (w->owned && w->dev) {
+    int cur = 0;
+    (void)hipGetDevice(&cur);
+    if (cur != w->device) (void)hipSetDevice(w->device);
+    (void)hipFree(w->dev);
+    if (cur != w->device) (void)hipSetDevice(cur);
+  }
+  delete w;
+}
+
+cq_status cq_weight_dims(const cq_weight* w, int64_t* n, int64_t* k) {
+  if (!w || !n || !k) return fail(CQ_ERR_NULL, "NULL argument");
+  *n = w->n;
+  *k = w->k;
+  return CQ_OK;
+}
+
+size_t cq_weight_vram_bytes(const cq_weight* w) { return w ? w->nbytes : 0; }
+const void* cq_weight_device_ptr(const cq_weight* w) { return w ? w->dev : nullptr; }
+
+static int gemv_waves(int units, long long row_tiles) {
+  int nw = env_int("COMBS_GEMV_WAVES", 0);
+  if (nw >= 1 && nw <= 16) return nw;
+  // Enough waves per workgroup that each handles ~2 units (one in flight
+  // while the previous one is computed), capped at 8 when the grid is large.
+  nw = (units + 1) / 2;
+  if (nw < 1) nw = 1;
+  const int cap = row_tiles >= 2048 ? 4 : (row_tiles >= 512 ? 8 : 16);
+  return nw > cap ? cap : nw;
+}
+
+static cq_status launch_gemv(DeviceModule* dm, const cq_weight* w, const void* x, int xt, int64_t m, void* y,
+                             int yt, hipStream_t s) {
+  const int fi = fmt_index(w->format);
+  const int qk = block_values(w->format);
+  const int64_t blocks = w->k / qk;
+  GemvArgs a;
+  a.w = w->dev;
+  a.x = x;
+  a.y = y;
+  a.row_bytes = (long long)(w->nbytes / (size_t)w->n);
+  a.M = (int)m;
+  a.N = (int)w->n;
+  a.K = (int)w->k;
+  a.units = (int)(qk == 256 ? blocks : (blocks + 3) / 4);
+  const long long row_tiles = (w->n + 15) / 16;
+  const long long m_tiles = (m + 15) / 16;
+  if (row_tiles > 0x7fffffffLL || m_tiles > 65535)
+    return fail(CQ_ERR_BAD_SHAPE, "grid too large (n=%lld, m=%lld)", (long long)w->n, (long long)m);
+  const int nw = gemv_waves(a.units, row_tiles);
+  void* params[] = {&a};
+  HIP_TRY(hipModuleLaunchKernel(dm->gemv[fi][xt][yt], (unsigned)row_tiles, (unsigned)m_tiles, 1, 64 * nw, 1, 1, 0,
+                                s, params, nullptr));
+  return CQ_OK;
+}
+
+cq_status cq_matmul_path(const cq_weight* w, const void* x, int x_dtype, int64_t m, void* y, int y_dtype, int path,
+                         void* stream) {
+  if (!w || !x || !y) return fail(CQ_ERR_NULL, "NULL weight, x or y");
+  if (x_dtype != CQ_F16 && x_dtype != CQ_F32) return fail(CQ_ERR_BAD_DTYPE, "x_dtype %d", x_dtype);
+  if (y_dtype != CQ_F16 && y_dtype != CQ_F32) return fail(CQ_ERR_BAD_DTYPE, "y_dtype %d", y_dtype);
+  if (m < 1 || m > (int64_t)0x7fffffff) return fail(CQ_ERR_BAD_SHAPE, "m=%lld must be >= 1", (long long)m);
+  if (path < CQ_PATH_AUTO || path > CQ_PATH_GEMM) return fail(CQ_ERR_BAD_SHAPE, "unknown path %d", path);
+  DeviceModule* dm;
+  cq_status st = device_module(&dm);
+  if (st != CQ_OK) return st;
+  return launch_gemv(dm, w, x, x_dtype == CQ_F32, m, y, y_dtype == CQ_F16, (hipStream_t)stream);
+}
+
+cq_status cq_matmul(const cq_weight* w, const void* x, int x_dtype, int64_t m, void* y, int y_dtype, void* stream) {
+  return cq_matmul_path(w, x, x_dtype, m, y, y_dtype, CQ_PATH_AUTO, stream);
+}
+
+cq_status cq_dequantize(int format, const void* device_bytes, size_t nbytes, int64_t n_values, float* device_out,
+                        void* stream) {
+  const int qk = block_values(format);
+  if (!qk) return fail(CQ_ERR_BAD_FORMAT, "unsupported format id %d", format);
+  if (!device_bytes || !device_out) return fail(CQ_ERR_NULL, "NULL buffer");
+  const size_t bb = (size_t)block_bytes(format);
+  if (nbytes == 0 || nbytes % bb != 0 || (int64_t)(nbytes / bb) * qk != n_values)
+    return fail(CQ_ERR_BAD_SHAPE, "%s dequant: %zu bytes is not %lld values", fmt_name(format), nbytes,
+                (long long)n_values);
+  DeviceModule* dm;
+  cq_status st = device_module(&dm);
+  if (st != CQ_OK) return st;
+  DequantArgs a{device_bytes, device_out, (long long)(n_values / 32)};
+  const long long blocks = (a.chunks + 255) / 256;
+  if (blocks > 0x7fffffffLL) return fail(CQ_ERR_BAD_SHAPE, "tensor too large");
+  void* params[] = {&a};
+  HIP_TRY(hipModuleLaunchKernel(dm->dequant[fmt_index(format)], (unsigned)blocks, 1, 1, 256, 1, 1, 0,
+                                (hipStream_t)stream, params, nullptr));
+  return CQ_OK;
+}
+
+const char* cq_last_error(void) { return g_err.c_str(); }
+const char* cq_version(void) { return "combs-qlinear 0.1.0 (gfx950)"; }
+
+}  // extern "C"

@@ -1,0 +1,39 @@
+// All device code of the library, compiled into one gfx950 code object
+// (hipcc --genco) that the host library embeds and loads with
+// hipModuleLoadData.  Kernel names are extern "C" so the host can look them
+// up with hipModuleGetFunction:
+//   cq_gemv_<fmt>_x<f16|f32>_y<f32|f16>   decode GEMV (m-tiles of 16)
+//   cq_dequant_<fmt>                      bit-exact dequantisation
+#include "cq_gemv.h"
+#include "cq_dequant.h"
+
+#define GEMV_KERNEL(NAME, FMT, XT, YT)                                               \
+  extern "C" __global__ void __launch_bounds__(1024) NAME(const GemvArgs a) { \
+    gemv_body<FMT, XT, YT>(a);                                                       \
+  }
+
+#define GEMV_FMT(fname, FMT)                          \
+  GEMV_KERNEL(cq_gemv_##fname##_xf16_yf32, FMT, 0, 0) \
+  GEMV_KERNEL(cq_gemv_##fname##_xf16_yf16, FMT, 0, 1) \
+  GEMV_KERNEL(cq_gemv_##fname##_xf32_yf32, FMT, 1, 0) \
+  GEMV_KERNEL(cq_gemv_##fname##_xf32_yf16, FMT, 1, 1)
+
+GEMV_FMT(q4_0, CQ_Q4_0)
+GEMV_FMT(q5_0, CQ_Q5_0)
+GEMV_FMT(q8_0, CQ_Q8_0)
+GEMV_FMT(q4_k, CQ_Q4_K)
+GEMV_FMT(q5_k, CQ_Q5_K)
+GEMV_FMT(q6_k, CQ_Q6_K)
+
+#define DEQUANT_KERNEL(fname, FMT)                                                  \
+  extern "C" __global__ void __launch_bounds__(256) cq_dequant_##fname(const DequantArgs a) { \
+    const long long c = (long long)blockIdx.x * blockDim.x + threadIdx.x;          \
+    if (c < a.chunks) dequant_chunk<FMT>(a.w, a.out, c);                            \
+  }
+
+DEQUANT_KERNEL(q4_0, CQ_Q4_0)
+DEQUANT_KERNEL(q5_0, CQ_Q5_0)
+DEQUANT_KERNEL(q8_0, CQ_Q8_0)
+DEQUANT_KERNEL(q4_k, CQ_Q4_K)
+DEQUANT_KERNEL(q5_k, CQ_Q5_K)
+DEQUANT_KERNEL(q6_k, CQ_Q6_K)

@@ -1,0 +1,143 @@
+"""GPU parity of the gfx950 kernels against the CPU oracle, through the C ABI.
+
+Mirrors the reference's own GPU tests (engine/core/combs-models/src/qmatmul.rs
+:1727-2174): bit-exact dequant, fused matmul vs ref_matmul(dequant) within
+|g - e| <= rel * max(|e|, 1) (rel 1e-4 for Q4_0, 1e-3 otherwise), at the
+reference's shapes, x patterns and synthetic block streams, plus ragged and
+multi-tile shapes, fp32/fp16 activations and outputs, and quantised N(0, 0.02)
+weights with N(0, 1) activations."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+from combsengine_amd import QuantFormat, QuantWeight, dequantize_gpu, quantize
+from combsengine_amd import _lib as L
+
+pytestmark = pytest.mark.gpu
+
+FMTS = [QuantFormat.Q4_0, QuantFormat.Q5_0, QuantFormat.Q8_0, QuantFormat.Q4K, QuantFormat.Q5K, QuantFormat.Q6K]
+LEGACY = {QuantFormat.Q4_0, QuantFormat.Q5_0, QuantFormat.Q8_0}
+
+
+def rel_of(fmt):
+    return 1e-4 if fmt == QuantFormat.Q4_0 else 1e-3
+
+
+def synth(fmt, n, k):
+    return O.SYNTH[int(fmt)](n * k // O.block_values(int(fmt)))
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_dequant_bit_exact_synth(cuda, fmt):
+    n_blocks = 33 if fmt in LEGACY else 9  # qmatmul.rs:1733, 1845: not a multiple of anything
+    data = O.SYNTH[int(fmt)](n_blocks)
+    n = n_blocks * O.block_values(int(fmt))
+    print(f"dequant {fmt.name} blocks={n_blocks}", flush=True)
+    got = dequantize_gpu(fmt, data)
+    want = O.dequant(int(fmt), data, n)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_dequant_bit_exact_quantized(cuda, fmt):
+    x = np.random.default_rng(int(fmt)).normal(0, 0.02, (37, 1024)).astype(np.float32)
+    data = quantize(fmt, x)
+    got = dequantize_gpu(fmt, data)
+    want = O.dequant(int(fmt), data, x.size)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_dequant_known_answers(cuda):
+    import json
+    gold = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "known_answers.json")))
+    for name, case in gold.items():
+        got = dequantize_gpu(case["format"], bytes.fromhex(case["hex"]))
+        assert np.array_equal(got, np.array(case["expect"], np.float32)), name
+
+
+def _run(w, x_np, x_dtype, y_dtype, path=L.CQ_PATH_AUTO):
+    import torch
+    x = torch.from_numpy(x_np).to("cuda").to(x_dtype)
+    y = torch.empty((x.shape[0], w.n_out()), dtype=y_dtype, device="cuda")
+    w.matmul_into(x, y, path=path)
+    return y.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_matmul_reference_shapes(cuda, fmt):
+    """qmatmul.rs:1751-1781 / 1893-1971 / 2019-2048: (67,128) legacy,
+    (35,512) K-quants, m in {1, 3}, x = ((i*7 % 13) - 6)/8."""
+    import torch
+    n, k = (67, 128) if fmt in LEGACY else (35, 512)
+    data = synth(fmt, n, k)
+    wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
+    w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
+    assert w.vram_bytes() == len(data)
+    for m in (1, 3):
+        x = O.x_pattern(m, k).reshape(m, k)
+        expect = O.ref_matmul(x, wd)
+        for xt in (torch.float32, torch.float16):
+            print(f"{fmt.name} n={n} k={k} m={m} x={xt}", flush=True)
+            O.assert_close(_run(w, x, xt, torch.float32), expect, rel_of(fmt), f"{fmt.name} m={m} x={xt}")
+        O.assert_close(w.matmul_host(x, m).reshape(m, n), expect, rel_of(fmt), "matmul_host")
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("m", [1, 2, 5, 16, 17, 40])
+def test_matmul_ragged_tiles(cuda, fmt, m):
+    """Ragged row tiles (n % 16 != 0), several K units per wave, m across
+    activation tiles; fp32 x (hi+lo split) and fp16 output."""
+    import torch
+    n, k = (300, 320) if fmt in LEGACY else (300, 1536)
+    data = synth(fmt, n, k)
+    wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
+    w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
+    x = O.x_pattern(m, k, 11, 29, 14.0, 16.0).reshape(m, k)
+    expect = O.ref_matmul(x, wd)
+    print(f"{fmt.name} n={n} k={k} m={m}", flush=True)
+    O.assert_close(_run(w, x, torch.float16, torch.float32), expect, 1e-3, "f16 x")
+    O.assert_close(_run(w, x, torch.float32, torch.float16), expect, 1e-3, "f16 y")
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_matmul_quantized_gaussian(cuda, fmt):
+    """N(0, 0.02) weights quantised with the GGUF quantiser, N(0, 1)
+    activations, fp16 and fp32 (split) activations."""
+    import torch
+    rng = np.random.default_rng(100 + int(fmt))
+    n, k, m = 200, 2048, 4
+    data = quantize(fmt, rng.normal(0, 0.02, (n, k)).astype(np.float32))
+    wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
+    w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
+    x32 = rng.normal(0, 1, (m, k)).astype(np.float32)
+    x16 = x32.astype(np.float16).astype(np.float32)
+    print(f"gaussian {fmt.name}", flush=True)
+    O.assert_close(_run(w, x16, torch.float16, torch.float32), O.ref_matmul(x16, wd), 1e-3, "x f16")
+    O.assert_close(_run(w, x32, torch.float32, torch.float32), O.ref_matmul(x32, wd), 1e-3, "x f32")
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_matmul_deterministic(cuda, fmt):
+    import torch
+    n, k = (300, 320) if fmt in LEGACY else (300, 1536)
+    w = QuantWeight.from_gguf_bytes(fmt, synth(fmt, n, k), n, k)
+    x = O.x_pattern(3, k).reshape(3, k)
+    a = _run(w, x, torch.float16, torch.float32)
+    b = _run(w, x, torch.float16, torch.float32)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_waves_override_consistent(cuda, monkeypatch):
+    """Different K splits across waves only reorder fp32 sums."""
+    import torch
+    fmt, n, k = QuantFormat.Q4K, 64, 4096
+    data = synth(fmt, n, k)
+    wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
+    w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
+    x = O.x_pattern(1, k).reshape(1, k)
+    expect = O.ref_matmul(x, wd)
+    for nw in ("1", "3", "8", "16"):
+        monkeypatch.setenv("COMBS_GEMV_WAVES", nw)
+        O.assert_close(_run(w, x, torch.float16, torch.float32), expect, 1e-3, f"nw={nw}")

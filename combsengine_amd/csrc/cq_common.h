@@ -48,6 +48,11 @@ __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel)
   return __builtin_amdgcn_perm(hi, lo, sel);
 }
 
+// (mask & a) | (~mask & b)  (v_bfi_b32)
+__device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) { return (mask & a) | (~mask & b); }
+// rotate right (v_alignbit_b32)
+__device__ __forceinline__ uint32_t rotr(uint32_t v, uint32_t s) { return __builtin_amdgcn_alignbit(v, v, s); }
+
 __device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
 __device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
 __device__ __forceinline__ h2 hsplat(float v) {
@@ -71,18 +76,20 @@ __device__ __forceinline__ f4 mfma(h8 a, h8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// One lane's slice of the activation matrix: row m of x (fp16 or fp32).
-// Lanes whose row is beyond M contribute zeros and touch no memory.
-// XT = 0: fp16 x used as is.  XT = 1: fp32 x split into hi + lo fp16 parts
-// (hi = fp16(x), lo = fp16(x - hi)), so the MFMA sees ~22 significant bits.
+// One lane's view of the activations staged in LDS as fp16: row m = (lane & 15)
+// of the current activation tile, for the K chunk starting at c0.  Lanes whose
+// row is beyond M read nothing and contribute zeros.
+// XT = 0: fp16 x as is.  XT = 1: fp32 x was split at staging time into
+// hi = fp16(x) and lo = fp16(x - hi), so the MFMA sees ~22 significant bits.
 template <int XT>
 struct XRow {
-  const uint8_t* base;
-  bool on;
-  __device__ XRow(const void* x, int m, int M, int K) {
-    on = m < M;
-    base = (const uint8_t*)x + (size_t)(on ? m : 0) * K * (XT ? 4 : 2);
-  }
+  const _Float16* hi;
+  const _Float16* lo;
+  // Lanes whose activation row is beyond M read row 0 instead: MFMA output
+  // row i depends only on A row i, and rows >= M are never stored, so no
+  // lane needs a branch or a zero fill.
+  __device__ XRow(const _Float16* hi_base, const _Float16* lo_base, int row, int stride, int c0, bool on)
+      : hi(hi_base + (on ? row : 0) * stride - c0), lo(lo_base + (on ? row : 0) * stride - c0) {}
 };
 
 template <int XT>
@@ -91,60 +98,28 @@ struct A8 {
   h8 lo;
 };
 
-template <int XT>
-__device__ __forceinline__ void cvt_split(const float* f, A8<XT>& a) {
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    _Float16 h = (_Float16)f[i];
-    a.hi[i] = h;
-    if (XT) a.lo[i] = (_Float16)(f[i] - (float)h);
-  }
-}
-
 // 8 consecutive activations starting at element k.
 template <int XT>
 __device__ __forceinline__ A8<XT> load_a8(const XRow<XT>& xr, int k) {
   A8<XT> a;
-  if (!XT) {
-    u4v v = xr.on ? ld_u128(xr.base + (size_t)k * 2) : u4v{0, 0, 0, 0};
-    a.hi = __builtin_bit_cast(h8, v);
-    a.lo = a.hi;
-  } else {
-    float f[8];
-    if (xr.on) {
-      u4v v0 = ld_u128(xr.base + (size_t)k * 4), v1 = ld_u128(xr.base + (size_t)k * 4 + 16);
-      __builtin_memcpy(f, &v0, 16);
-      __builtin_memcpy(f + 4, &v1, 16);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; i++) f[i] = 0.0f;
-    }
-    cvt_split<XT>(f, a);
-  }
+  a.hi = *(const h8*)(xr.hi + k);
+  a.lo = XT ? *(const h8*)(xr.lo + k) : a.hi;
   return a;
 }
+
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 
 // 4 activations at k0 followed by 4 at k1.
 template <int XT>
 __device__ __forceinline__ A8<XT> load_a4x2(const XRow<XT>& xr, int k0, int k1) {
   A8<XT> a;
-  if (!XT) {
-    u2v p = xr.on ? ld_u64(xr.base + (size_t)k0 * 2) : u2v{0, 0};
-    u2v q = xr.on ? ld_u64(xr.base + (size_t)k1 * 2) : u2v{0, 0};
-    u4v v = {p.x, p.y, q.x, q.y};
-    a.hi = __builtin_bit_cast(h8, v);
-    a.lo = a.hi;
+  const h4 p = *(const h4*)(xr.hi + k0), q = *(const h4*)(xr.hi + k1);
+  a.hi = __builtin_shufflevector(p, q, 0, 1, 2, 3, 4, 5, 6, 7);
+  if (XT) {
+    const h4 pl = *(const h4*)(xr.lo + k0), ql = *(const h4*)(xr.lo + k1);
+    a.lo = __builtin_shufflevector(pl, ql, 0, 1, 2, 3, 4, 5, 6, 7);
   } else {
-    float f[8];
-    if (xr.on) {
-      u4v v0 = ld_u128(xr.base + (size_t)k0 * 4), v1 = ld_u128(xr.base + (size_t)k1 * 4);
-      __builtin_memcpy(f, &v0, 16);
-      __builtin_memcpy(f + 4, &v1, 16);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; i++) f[i] = 0.0f;
-    }
-    cvt_split<XT>(f, a);
+    a.lo = a.hi;
   }
   return a;
 }

@@ -28,6 +28,8 @@ struct GemvArgs {
   long long row_bytes;
   int M, N, K;
   int units;          // work units per row
+  int kc;             // K values per LDS chunk of activations (multiple of a unit)
+  int lds_stride;     // halves per staged activation row (kc + 8)
 };
 
 // Byte selectors for v_perm_b32(hi, lo, sel): byte i of the result takes
@@ -36,6 +38,11 @@ struct GemvArgs {
 #define SEL_B2_B3 0x0c030c02u   // [lo.b2, 0, lo.b3, 0]
 #define SEL_X_B01 0x05010400u   // [lo.b0, hi.b0, lo.b1, hi.b1]
 #define SEL_X_B23 0x07030602u   // [lo.b2, hi.b2, lo.b3, hi.b3]
+#define SEL_B0_E_B1_E 0x04010400u  // [lo.b0, hi.b0, lo.b1, hi.b0]: hi = C64 puts 0x64 above each byte
+#define SEL_B2_E_B3_E 0x04030402u
+// fp16 exponent byte of 1024: perm(C64, w, SEL_B*_E_*) turns bytes of w into
+// the halves 0x64bb, i.e. fp16 1024 + b, and an AND keeps the wanted bits.
+#define C64 0x64646464u
 
 // ---------------------------------------------------------------------------
 // Q4_K: 144-byte superblock [d f16][dmin f16][scales 12][qs 128]
@@ -67,19 +74,15 @@ __device__ __forceinline__ void compute_q4k(const FragQ4K& f, const XRow<XT>& xr
 #pragma unroll
   for (int s = 0; s < 8; s++) {
     const uint32_t wa = w[2 * (s & 3)], wb = w[2 * (s & 3) + 1];
-    const uint32_t pa1 = perm(0, wa, SEL_B0_B1), pa2 = perm(0, wa, SEL_B2_B3);
-    const uint32_t pb1 = perm(0, wb, SEL_B0_B1), pb2 = perm(0, wb, SEL_B2_B3);
+    const uint32_t pa1 = perm(C64, wa, SEL_B0_E_B1_E), pa2 = perm(C64, wa, SEL_B2_E_B3_E);
+    const uint32_t pb1 = perm(C64, wb, SEL_B0_E_B1_E), pb2 = perm(C64, wb, SEL_B2_E_B3_E);
     h8 b;
     if (s < 4) {
-      b = mk_h8(pk_fma((pa1 & 0x000F000Fu) | 0x64006400u, s_lo, c_lo),
-                pk_fma((pa2 & 0x000F000Fu) | 0x64006400u, s_lo, c_lo),
-                pk_fma((pb1 & 0x000F000Fu) | 0x64006400u, s_lo, c_lo),
-                pk_fma((pb2 & 0x000F000Fu) | 0x64006400u, s_lo, c_lo));
+      b = mk_h8(pk_fma(pa1 & 0x640F640Fu, s_lo, c_lo), pk_fma(pa2 & 0x640F640Fu, s_lo, c_lo),
+                pk_fma(pb1 & 0x640F640Fu, s_lo, c_lo), pk_fma(pb2 & 0x640F640Fu, s_lo, c_lo));
     } else {
-      b = mk_h8(pk_fma((pa1 & 0x00F000F0u) | 0x64006400u, s_hi, c_hi),
-                pk_fma((pa2 & 0x00F000F0u) | 0x64006400u, s_hi, c_hi),
-                pk_fma((pb1 & 0x00F000F0u) | 0x64006400u, s_hi, c_hi),
-                pk_fma((pb2 & 0x00F000F0u) | 0x64006400u, s_hi, c_hi));
+      b = mk_h8(pk_fma(pa1 & 0x64F064F0u, s_hi, c_hi), pk_fma(pa2 & 0x64F064F0u, s_hi, c_hi),
+                pk_fma(pb1 & 0x64F064F0u, s_hi, c_hi), pk_fma(pb2 & 0x64F064F0u, s_hi, c_hi));
     }
     const A8<XT> a = load_a8<XT>(xr, k0 + 64 * g + 8 * s);
     c = mfma_x<XT>(a, b, c);
@@ -115,7 +118,7 @@ __device__ __forceinline__ void compute_q5k(const FragQ5K& f, const XRow<XT>& xr
   const h8 bm0 = mk_h8(um0, um0, um0, um0), bm1 = mk_h8(um1, um1, um1, um1);
   const uint32_t w[8] = {f.q0.x, f.q0.y, f.q0.z, f.q0.w, f.q1.x, f.q1.y, f.q1.z, f.q1.w};
   const uint32_t hb[8] = {f.h0.x, f.h0.y, f.h0.z, f.h0.w, f.h1.x, f.h1.y, f.h1.z, f.h1.w};
-  const int shl = 2 * g, shh = 2 * g + 1;
+  const int rl = (2 * g - 4) & 31, shh = 2 * g + 1;
   f4 c = {0, 0, 0, 0}, cm = {0, 0, 0, 0};
 #pragma unroll
   for (int s = 0; s < 8; s++) {
@@ -125,15 +128,15 @@ __device__ __forceinline__ void compute_q5k(const FragQ5K& f, const XRow<XT>& xr
     for (int e = 0; e < 2; e++) {
       const uint32_t wq = w[i0 + e], hq = hb[i0 + e];
       if (s < 4) {
-        // bit 2g of each qh byte -> bit 4 of the byte, merged under the low nibble.
-        const uint32_t z = (wq & 0x0F0F0F0Fu) | (((hq >> shl) << 4) & 0x10101010u);
-        u[2 * e] = pk_fma((perm(0, z, SEL_B0_B1) & 0x001F001Fu) | 0x64006400u, s_lo, c_lo);
-        u[2 * e + 1] = pk_fma((perm(0, z, SEL_B2_B3) & 0x001F001Fu) | 0x64006400u, s_lo, c_lo);
+        // rotate bit 2g of each qh byte to bit 4 and insert it above the low nibble
+        const uint32_t z = bfi(0x10101010u, rotr(hq, rl), wq);
+        u[2 * e] = pk_fma(perm(C64, z, SEL_B0_E_B1_E) & 0x641F641Fu, s_lo, c_lo);
+        u[2 * e + 1] = pk_fma(perm(C64, z, SEL_B2_E_B3_E) & 0x641F641Fu, s_lo, c_lo);
       } else {
-        // high nibble at bits 4-7 of the half, bit 2g+1 of qh at bit 8.
-        const uint32_t hx = hq >> shh;
-        u[2 * e] = pk_fma((perm(hx, wq, SEL_X_B01) & 0x01F001F0u) | 0x64006400u, s_hi, c_hi);
-        u[2 * e + 1] = pk_fma((perm(hx, wq, SEL_X_B23) & 0x01F001F0u) | 0x64006400u, s_hi, c_hi);
+        // high nibble at bits 4-7 of the half, bit 2g+1 of qh at bit 8 under 0x64
+        const uint32_t hx = ((hq >> shh) & 0x01010101u) | C64;
+        u[2 * e] = pk_fma(perm(hx, wq, SEL_X_B01) & 0x65F065F0u, s_hi, c_hi);
+        u[2 * e + 1] = pk_fma(perm(hx, wq, SEL_X_B23) & 0x65F065F0u, s_hi, c_hi);
       }
     }
     const h8 b = mk_h8(u[0], u[1], u[2], u[3]);
@@ -197,14 +200,14 @@ __device__ __forceinline__ void compute_q6k(const FragQ6K& f, const XRow<XT>& xr
         uint32_t v1, v2;
         if (t < 2) {
           // qh bits 2t,2t+1 -> bits 4,5 of each byte, under the low nibble
-          const uint32_t z = (wq & 0x0F0F0F0Fu) | ((hq << (4 - 2 * t)) & 0x30303030u);
-          v1 = (perm(0, z, SEL_B0_B1) & 0x003F003Fu) | 0x64006400u;
-          v2 = (perm(0, z, SEL_B2_B3) & 0x003F003Fu) | 0x64006400u;
+          const uint32_t z = bfi(0x30303030u, hq << (4 - 2 * t), wq);
+          v1 = perm(C64, z, SEL_B0_E_B1_E) & 0x643F643Fu;
+          v2 = perm(C64, z, SEL_B2_E_B3_E) & 0x643F643Fu;
         } else {
-          // high nibble at bits 4-7, qh bits 2t,2t+1 at bits 8,9
-          const uint32_t hx = hq >> (2 * t);
-          v1 = (perm(hx, wq, SEL_X_B01) & 0x03F003F0u) | 0x64006400u;
-          v2 = (perm(hx, wq, SEL_X_B23) & 0x03F003F0u) | 0x64006400u;
+          // high nibble at bits 4-7, qh bits 2t,2t+1 at bits 8,9 under 0x64
+          const uint32_t hx = ((hq >> (2 * t)) & 0x03030303u) | C64;
+          v1 = perm(hx, wq, SEL_X_B01) & 0x67F067F0u;
+          v2 = perm(hx, wq, SEL_X_B23) & 0x67F067F0u;
         }
         uh[2 * i] = pk_fma(v1, sh_s, sh_c);
         uh[2 * i + 1] = pk_fma(v2, sh_s, sh_c);
@@ -246,11 +249,9 @@ __device__ __forceinline__ void compute_q40(const FragQ40& f, const XRow<XT>& xr
 #pragma unroll
   for (int i = 0; i < LB; i++) {
     if (i >= nb) break;
-    const uint32_t p1 = perm(0, f.q[i], SEL_B0_B1), p2 = perm(0, f.q[i], SEL_B2_B3);
-    const h8 b = mk_h8(pk_fma((p1 & 0x000F000Fu) | 0x64006400u, one, c_lo),
-                       pk_fma((p2 & 0x000F000Fu) | 0x64006400u, one, c_lo),
-                       pk_fma((p1 & 0x00F000F0u) | 0x64006400u, s16, c_hi),
-                       pk_fma((p2 & 0x00F000F0u) | 0x64006400u, s16, c_hi));
+    const uint32_t p1 = perm(C64, f.q[i], SEL_B0_E_B1_E), p2 = perm(C64, f.q[i], SEL_B2_E_B3_E);
+    const h8 b = mk_h8(pk_fma(p1 & 0x640F640Fu, one, c_lo), pk_fma(p2 & 0x640F640Fu, one, c_lo),
+                       pk_fma(p1 & 0x64F064F0u, s16, c_hi), pk_fma(p2 & 0x64F064F0u, s16, c_hi));
     const int kb = k0 + 32 * i;
     const A8<XT> a = load_a4x2<XT>(xr, kb + 4 * g, kb + 16 + 4 * g);
     const f4 c = mfma_x<XT>(a, b, f4{0, 0, 0, 0});
@@ -289,11 +290,12 @@ __device__ __forceinline__ void compute_q50(const FragQ50& f, const XRow<XT>& xr
     const uint32_t q = f.q[i];
     const uint32_t hl = spread4(f.h[i] >> (4 * g));
     const uint32_t hh = spread4(f.h[i] >> (16 + 4 * g));
-    const uint32_t z = (q & 0x0F0F0F0Fu) | (hl << 4);
-    const h8 b = mk_h8(pk_fma((perm(0, z, SEL_B0_B1) & 0x001F001Fu) | 0x64006400u, one, c_lo),
-                       pk_fma((perm(0, z, SEL_B2_B3) & 0x001F001Fu) | 0x64006400u, one, c_lo),
-                       pk_fma((perm(hh, q, SEL_X_B01) & 0x01F001F0u) | 0x64006400u, s16, c_hi),
-                       pk_fma((perm(hh, q, SEL_X_B23) & 0x01F001F0u) | 0x64006400u, s16, c_hi));
+    const uint32_t z = bfi(0x10101010u, hl << 4, q);
+    const uint32_t hx = hh | C64;
+    const h8 b = mk_h8(pk_fma(perm(C64, z, SEL_B0_E_B1_E) & 0x641F641Fu, one, c_lo),
+                       pk_fma(perm(C64, z, SEL_B2_E_B3_E) & 0x641F641Fu, one, c_lo),
+                       pk_fma(perm(hx, q, SEL_X_B01) & 0x65F065F0u, s16, c_hi),
+                       pk_fma(perm(hx, q, SEL_X_B23) & 0x65F065F0u, s16, c_hi));
     const int kb = k0 + 32 * i;
     const A8<XT> a = load_a4x2<XT>(xr, kb + 4 * g, kb + 16 + 4 * g);
     const f4 c = mfma_x<XT>(a, b, f4{0, 0, 0, 0});
@@ -367,38 +369,141 @@ __device__ __forceinline__ void compute_unit(const typename FmtTraits<FMT>::Frag
   else compute_q80<XT>(f, xr, k0, g, nb, acc);
 }
 
-#define CQ_MAX_WAVES 16
+#define CQ_MAX_WAVES 8
+#define CQ_DEPTH 4  // units of weight loads a wave keeps in flight
+
+// Activation staging, split in two so the weight loads can be issued in
+// between: issue() loads up to XS_REG 8-value vectors per thread into
+// registers, commit() converts and stores them to LDS (waiting only for those
+// loads, which were issued first), and stage_rest() covers any remainder with
+// a plain loop.
+#define XS_REG 4
+template <int XT>
+struct XStage {
+  u4v v[XS_REG][XT ? 2 : 1];
+};
+
+template <int XT>
+__device__ __forceinline__ void stage_issue(const GemvArgs& a, XStage<XT>& st, int m0, int mt, int c0, int len) {
+  const int vec = len >> 3, total = mt * vec;
+#pragma unroll
+  for (int q = 0; q < XS_REG; q++) {
+    int i = threadIdx.x + q * blockDim.x;
+    i = i < total ? i : total - 1;  // clamp: valid address, store skipped
+    const int r = i / vec, v = i - r * vec;
+    const size_t src = (size_t)(m0 + r) * a.K + c0 + 8 * v;
+    if (!XT) {
+      st.v[q][0] = ld_u128((const uint8_t*)a.x + src * 2);
+    } else {
+      st.v[q][0] = ld_u128((const uint8_t*)a.x + src * 4);
+      st.v[q][XT] = ld_u128((const uint8_t*)a.x + src * 4 + 16);
+    }
+  }
+}
+
+template <int XT>
+__device__ __forceinline__ void stage_store(const GemvArgs& a, _Float16* hi, _Float16* lo, int i, int vec,
+                                            const u4v* src) {
+  const int r = i / vec, v = i - r * vec;
+  _Float16* dh = hi + r * a.lds_stride + 8 * v;
+  if (!XT) {
+    *(u4v*)dh = src[0];
+  } else {
+    float f[8];
+    __builtin_memcpy(f, &src[0], 16);
+    __builtin_memcpy(f + 4, &src[XT], 16);
+    h8 vh, vl;
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      vh[q] = (_Float16)f[q];
+      vl[q] = (_Float16)(f[q] - (float)vh[q]);
+    }
+    *(h8*)dh = vh;
+    *(h8*)(lo + r * a.lds_stride + 8 * v) = vl;
+  }
+}
+
+template <int XT>
+__device__ __forceinline__ void stage_commit(const GemvArgs& a, const XStage<XT>& st, _Float16* hi, _Float16* lo,
+                                             int m0, int mt, int c0, int len) {
+  const int vec = len >> 3, total = mt * vec;
+#pragma unroll
+  for (int q = 0; q < XS_REG; q++) {
+    const int i = threadIdx.x + q * blockDim.x;
+    if (i < total) stage_store<XT>(a, hi, lo, i, vec, st.v[q]);
+  }
+  for (int i = threadIdx.x + XS_REG * blockDim.x; i < total; i += blockDim.x) {
+    const size_t src = (size_t)(m0 + i / vec) * a.K + c0 + 8 * (i % vec);
+    u4v t[2];
+    if (!XT) {
+      t[0] = ld_u128((const uint8_t*)a.x + src * 2);
+    } else {
+      t[0] = ld_u128((const uint8_t*)a.x + src * 4);
+      t[1] = ld_u128((const uint8_t*)a.x + src * 4 + 16);
+    }
+    stage_store<XT>(a, hi, lo, i, vec, t);
+  }
+}
 
 // Grid: x = ceil(N/16) row tiles, y = ceil(M/16) activation tiles.
-// Block: 64 * nw threads, nw in 1..16.
+// Block: 64 * nw threads, nw in 1..8.  Dynamic LDS: (XT ? 2 : 1) * mt *
+// lds_stride halves, mt = min(16, M).
 template <int FMT, int XT, int YT>
 __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
   typedef FmtTraits<FMT> T;
+  typedef typename T::Frag Frag;
   __shared__ float red[CQ_MAX_WAVES][4][64];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  extern __shared__ __attribute__((aligned(16))) _Float16 xs[];
+  // wave index is uniform across the wave: keep it (and the unit loop) scalar
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
   const int j = lane & 15, g = lane >> 4;
   const int n0 = blockIdx.x * 16, m0 = blockIdx.y * 16;
+  const int mt = min(16, a.M - m0);
+  const int mrows = min(16, a.M);  // rows allocated in LDS
+  _Float16* xhi = xs;
+  _Float16* xlo = xs + mrows * a.lds_stride;
   const int row = min(n0 + j, a.N - 1);
   const uint8_t* wr = a.w + (size_t)row * a.row_bytes;
-  const XRow<XT> xr(a.x, m0 + j, a.M, a.K);
-  // legacy formats: blocks in the last (ragged) unit of the row
   const int blocks = a.K / 32;
   f4 acc = {0, 0, 0, 0};
-  typename T::Frag cur, nxt;
-  int u = wave;
-  if (u < a.units) {
-    const int nb = (T::vals == 256) ? 0 : min(LB, blocks - u * LB);
-    load_unit<FMT>(cur, wr + (size_t)u * T::bytes, g, nb);
-  }
-  for (; u < a.units; u += nw) {
-    const int nb = (T::vals == 256) ? 0 : min(LB, blocks - u * LB);
-    const int un = u + nw;
-    if (un < a.units) {
-      const int nbn = (T::vals == 256) ? 0 : min(LB, blocks - un * LB);
-      load_unit<FMT>(nxt, wr + (size_t)un * T::bytes, g, nbn);
+  for (int c0 = 0; c0 < a.K; c0 += a.kc) {
+    const int len = min(a.kc, a.K - c0);
+    const int u_end = (c0 + len + T::vals - 1) / T::vals;
+    int ub = c0 / T::vals + wave;
+    Frag f[CQ_DEPTH];
+    // Issue order matters: vmcnt retires loads in order, so the activation
+    // loads go first (the LDS store waits only for them), then one group of
+    // weight loads; unit d's compute then waits only for its own loads.
+    XStage<XT> st;
+    stage_issue<XT>(a, st, m0, mt, c0, len);
+#pragma unroll
+    for (int d = 0; d < CQ_DEPTH; d++) {
+      const int u = min(ub + d * nw, u_end - 1);  // past the end: reload a valid unit, skip its compute
+      const int nb = (T::vals == 256) ? 0 : min(LB, blocks - u * LB);
+      load_unit<FMT>(f[d], wr + (size_t)u * T::bytes, g, nb);
     }
-    compute_unit<FMT, XT>(cur, xr, u * T::vals, g, nb, acc);
-    cur = nxt;
+    if (c0 > 0) __syncthreads();  // previous chunk fully consumed
+    stage_commit<XT>(a, st, xhi, xlo, m0, mt, c0, len);
+    __syncthreads();
+    const XRow<XT> xr(xhi, xlo, j, a.lds_stride, c0, j < mt);
+    while (true) {
+#pragma unroll
+      for (int d = 0; d < CQ_DEPTH; d++) {
+        const int u = ub + d * nw;
+        if (u < u_end) {
+          const int nb = (T::vals == 256) ? 0 : min(LB, blocks - u * LB);
+          compute_unit<FMT, XT>(f[d], xr, u * T::vals, g, nb, acc);
+        }
+      }
+      ub += CQ_DEPTH * nw;
+      if (ub >= u_end) break;
+#pragma unroll
+      for (int d = 0; d < CQ_DEPTH; d++) {
+        const int u = min(ub + d * nw, u_end - 1);
+        const int nb = (T::vals == 256) ? 0 : min(LB, blocks - u * LB);
+        load_unit<FMT>(f[d], wr + (size_t)u * T::bytes, g, nb);
+      }
+    }
   }
   if (nw > 1) {
 #pragma unroll

@@ -104,6 +104,8 @@ struct GemvArgs {
   long long row_bytes;
   int M, N, K;
   int units;
+  int kc;
+  int lds_stride;
 };
 struct DequantArgs {
   const void* w;
@@ -270,15 +272,18 @@ cq_status cq_weight_dims(const cq_weight* w, int64_t* n, int64_t* k) {
 size_t cq_weight_vram_bytes(const cq_weight* w) { return w ? w->nbytes : 0; }
 const void* cq_weight_device_ptr(const cq_weight* w) { return w ? w->dev : nullptr; }
 
-static int gemv_waves(int units, long long row_tiles) {
+// Units of weight loads each wave keeps in flight (CQ_DEPTH in cq_gemv.h).
+constexpr int kGemvDepth = 4;
+// LDS for the staged activations (the kernel also holds 8 KB of reduction
+// space; the total stays within the default 64 KB per workgroup).
+constexpr int kGemvLdsBudget = 56 * 1024;
+
+static int gemv_waves(int units) {
   int nw = env_int("COMBS_GEMV_WAVES", 0);
-  if (nw >= 1 && nw <= 16) return nw;
-  // Enough waves per workgroup that each handles ~2 units (one in flight
-  // while the previous one is computed), capped at 8 when the grid is large.
-  nw = (units + 1) / 2;
-  if (nw < 1) nw = 1;
-  const int cap = row_tiles >= 2048 ? 4 : (row_tiles >= 512 ? 8 : 16);
-  return nw > cap ? cap : nw;
+  if (nw >= 1 && nw <= 8) return nw;
+  // one group of kGemvDepth units per wave where possible, at most 8 waves
+  nw = (units + kGemvDepth - 1) / kGemvDepth;
+  return nw < 1 ? 1 : (nw > 8 ? 8 : nw);
 }
 
 static cq_status launch_gemv(DeviceModule* dm, const cq_weight* w, const void* x, int xt, int64_t m, void* y,
@@ -286,6 +291,7 @@ static cq_status launch_gemv(DeviceModule* dm, const cq_weight* w, const void* x
   const int fi = fmt_index(w->format);
   const int qk = block_values(w->format);
   const int64_t blocks = w->k / qk;
+  const int unit_vals = qk == 256 ? 256 : 128;  // K-quant superblock or 4 legacy blocks
   GemvArgs a;
   a.w = w->dev;
   a.x = x;
@@ -295,14 +301,23 @@ static cq_status launch_gemv(DeviceModule* dm, const cq_weight* w, const void* x
   a.N = (int)w->n;
   a.K = (int)w->k;
   a.units = (int)(qk == 256 ? blocks : (blocks + 3) / 4);
+  const int mrows = m < 16 ? (int)m : 16;
+  const int xmul = xt ? 2 : 1;
+  int kc = kGemvLdsBudget / (2 * xmul * mrows) - 8;
+  kc -= kc % unit_vals;
+  const int k_units = (int)((w->k + unit_vals - 1) / unit_vals) * unit_vals;
+  if (kc > k_units) kc = k_units;
+  a.kc = kc;
+  a.lds_stride = kc + 8;
+  const size_t lds = (size_t)xmul * mrows * a.lds_stride * 2;
   const long long row_tiles = (w->n + 15) / 16;
   const long long m_tiles = (m + 15) / 16;
   if (row_tiles > 0x7fffffffLL || m_tiles > 65535)
     return fail(CQ_ERR_BAD_SHAPE, "grid too large (n=%lld, m=%lld)", (long long)w->n, (long long)m);
-  const int nw = gemv_waves(a.units, row_tiles);
+  const int nw = gemv_waves(a.units);
   void* params[] = {&a};
-  HIP_TRY(hipModuleLaunchKernel(dm->gemv[fi][xt][yt], (unsigned)row_tiles, (unsigned)m_tiles, 1, 64 * nw, 1, 1, 0,
-                                s, params, nullptr));
+  HIP_TRY(hipModuleLaunchKernel(dm->gemv[fi][xt][yt], (unsigned)row_tiles, (unsigned)m_tiles, 1, 64 * nw, 1, 1,
+                                (unsigned)lds, s, params, nullptr));
   return CQ_OK;
 }
 

@@ -8,7 +8,7 @@
 #include "cq_dequant.h"
 
 #define GEMV_KERNEL(NAME, FMT, XT, YT)                                               \
-  extern "C" __global__ void __launch_bounds__(1024) NAME(const GemvArgs a) { \
+  extern "C" __global__ void __launch_bounds__(512) NAME(const GemvArgs a) { \
     gemv_body<FMT, XT, YT>(a);                                                       \
   }
 

@@ -378,6 +378,13 @@ __device__ __forceinline__ void compute_unit(const typename FmtTraits<FMT>::Frag
 // loads, which were issued first), and stage_rest() covers any remainder with
 // a plain loop.
 #define XS_REG 4
+
+// i / vec for 0 <= i < 16 * vec <= 2^20: the quotient through a float
+// reciprocal is exact here ((i + 0.5) / vec is at least 0.5 / vec away from
+// an integer, far above the float rounding error), and costs 3 VALU ops
+// instead of an integer division sequence.
+__device__ __forceinline__ int div_small(int i, float rcp) { return (int)(((float)i + 0.5f) * rcp); }
+
 template <int XT>
 struct XStage {
   u4v v[XS_REG][XT ? 2 : 1];
@@ -386,25 +393,27 @@ struct XStage {
 template <int XT>
 __device__ __forceinline__ void stage_issue(const GemvArgs& a, XStage<XT>& st, int m0, int mt, int c0, int len) {
   const int vec = len >> 3, total = mt * vec;
+  const float rcp = 1.0f / (float)vec;
 #pragma unroll
   for (int q = 0; q < XS_REG; q++) {
     int i = threadIdx.x + q * blockDim.x;
     i = i < total ? i : total - 1;  // clamp: valid address, store skipped
-    const int r = i / vec, v = i - r * vec;
-    const size_t src = (size_t)(m0 + r) * a.K + c0 + 8 * v;
+    const int r = div_small(i, rcp), v = i - r * vec;
+    // byte offsets of x fit 31 bits (checked on the host)
+    const uint32_t src = (uint32_t)((m0 + r) * a.K + c0 + 8 * v) * (XT ? 4u : 2u);
     if (!XT) {
-      st.v[q][0] = ld_u128((const uint8_t*)a.x + src * 2);
+      st.v[q][0] = ld_u128((const uint8_t*)a.x + src);
     } else {
-      st.v[q][0] = ld_u128((const uint8_t*)a.x + src * 4);
-      st.v[q][XT] = ld_u128((const uint8_t*)a.x + src * 4 + 16);
+      st.v[q][0] = ld_u128((const uint8_t*)a.x + src);
+      st.v[q][XT] = ld_u128((const uint8_t*)a.x + src + 16);
     }
   }
 }
 
 template <int XT>
 __device__ __forceinline__ void stage_store(const GemvArgs& a, _Float16* hi, _Float16* lo, int i, int vec,
-                                            const u4v* src) {
-  const int r = i / vec, v = i - r * vec;
+                                            float rcp, const u4v* src) {
+  const int r = div_small(i, rcp), v = i - r * vec;
   _Float16* dh = hi + r * a.lds_stride + 8 * v;
   if (!XT) {
     *(u4v*)dh = src[0];
@@ -427,21 +436,19 @@ template <int XT>
 __device__ __forceinline__ void stage_commit(const GemvArgs& a, const XStage<XT>& st, _Float16* hi, _Float16* lo,
                                              int m0, int mt, int c0, int len) {
   const int vec = len >> 3, total = mt * vec;
+  const float rcp = 1.0f / (float)vec;
 #pragma unroll
   for (int q = 0; q < XS_REG; q++) {
     const int i = threadIdx.x + q * blockDim.x;
-    if (i < total) stage_store<XT>(a, hi, lo, i, vec, st.v[q]);
+    if (i < total) stage_store<XT>(a, hi, lo, i, vec, rcp, st.v[q]);
   }
   for (int i = threadIdx.x + XS_REG * blockDim.x; i < total; i += blockDim.x) {
-    const size_t src = (size_t)(m0 + i / vec) * a.K + c0 + 8 * (i % vec);
+    const int r = div_small(i, rcp);
+    const uint32_t src = (uint32_t)((m0 + r) * a.K + c0 + 8 * (i - r * vec)) * (XT ? 4u : 2u);
     u4v t[2];
-    if (!XT) {
-      t[0] = ld_u128((const uint8_t*)a.x + src * 2);
-    } else {
-      t[0] = ld_u128((const uint8_t*)a.x + src * 4);
-      t[1] = ld_u128((const uint8_t*)a.x + src * 4 + 16);
-    }
-    stage_store<XT>(a, hi, lo, i, vec, t);
+    t[0] = ld_u128((const uint8_t*)a.x + src);
+    if (XT) t[1] = ld_u128((const uint8_t*)a.x + src + 16);
+    stage_store<XT>(a, hi, lo, i, vec, rcp, t);
   }
 }
 

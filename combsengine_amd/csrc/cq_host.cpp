@@ -328,6 +328,8 @@ cq_status cq_matmul_path(const cq_weight* w, const void* x, int x_dtype, int64_t
   if (y_dtype != CQ_F16 && y_dtype != CQ_F32) return fail(CQ_ERR_BAD_DTYPE, "y_dtype %d", y_dtype);
   if (m < 1 || m > (int64_t)0x7fffffff) return fail(CQ_ERR_BAD_SHAPE, "m=%lld must be >= 1", (long long)m);
   if (path < CQ_PATH_AUTO || path > CQ_PATH_GEMM) return fail(CQ_ERR_BAD_SHAPE, "unknown path %d", path);
+  if ((uint64_t)m * (uint64_t)w->k * (x_dtype == CQ_F32 ? 4u : 2u) >= (1ull << 31))
+    return fail(CQ_ERR_BAD_SHAPE, "activations of %lld x %lld exceed 2 GiB", (long long)m, (long long)w->k);
   DeviceModule* dm;
   cq_status st = device_module(&dm);
   if (st != CQ_OK) return st;

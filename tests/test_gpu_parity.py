@@ -141,3 +141,16 @@ def test_waves_override_consistent(cuda, monkeypatch):
     for nw in ("1", "3", "5", "8"):
         monkeypatch.setenv("COMBS_GEMV_WAVES", nw)
         O.assert_close(_run(w, x, torch.float16, torch.float32), expect, 1e-3, f"nw={nw}")
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("n,k,m", [(4100, 512, 1), (70, 7168, 2), (8200, 2048, 3)])
+def test_gemv_large_and_ragged(cuda, fmt, n, k, m):
+    """Many row tiles, many K units per wave, ragged tiles."""
+    import torch
+    data = synth(fmt, n, k)
+    wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
+    w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
+    x = O.x_pattern(m, k, 13, 31, 15.0, 16.0).reshape(m, k)
+    print(f"{fmt.name} n={n} k={k} m={m}", flush=True)
+    O.assert_close(_run(w, x, torch.float16, torch.float32), O.ref_matmul(x, wd), 1e-3, "gemv")

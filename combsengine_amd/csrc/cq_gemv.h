@@ -59,38 +59,61 @@ __device__ __forceinline__ void load_q4k(FragQ4K& f, const uint8_t* sb, int g) {
   f.q0 = ld_u128(sb + 16 + 32 * g);
   f.q1 = ld_u128(sb + 32 + 32 * g);
 }
-template <int XT>
-__device__ __forceinline__ void compute_q4k(const FragQ4K& f, const XRow<XT>& xr, int k0, int g, f4& acc) {
+// MFMA B operands of one Q4_K superblock for this lane: b[s] for step s
+// (k = 64g + 8s .. +7), the per-lane min operands for the two sub-blocks it
+// holds (fp16 pairs), and the superblock scales.
+struct DecKQ {
+  h8 b[8];
+  uint32_t um0, um1;
+  float d, dmin;
+};
+__device__ __forceinline__ void decode_q4k(const FragQ4K& f, int g, DecKQ& o) {
   uint32_t sc0, m0, sc1, m1;
   scale_min_k4(2 * g, f.hdr.y, f.hdr.z, f.hdr.w, sc0, m0);
   scale_min_k4(2 * g + 1, f.hdr.y, f.hdr.z, f.hdr.w, sc1, m1);
   const h2 s_lo = hsplat((float)sc0), c_lo = hsplat(-1024.0f * (float)sc0);
   const h2 s_hi = hsplat((float)sc1 * 0.0625f), c_hi = hsplat(-64.0f * (float)sc1);
-  const h2 mn0 = hsplat((float)m0), mn1 = hsplat((float)m1);
-  const uint32_t um0 = as_u32(mn0), um1 = as_u32(mn1);
-  const h8 bm0 = mk_h8(um0, um0, um0, um0), bm1 = mk_h8(um1, um1, um1, um1);
+  o.um0 = as_u32(hsplat((float)m0));
+  o.um1 = as_u32(hsplat((float)m1));
   const uint32_t w[8] = {f.q0.x, f.q0.y, f.q0.z, f.q0.w, f.q1.x, f.q1.y, f.q1.z, f.q1.w};
-  f4 c = {0, 0, 0, 0}, cm = {0, 0, 0, 0};
 #pragma unroll
   for (int s = 0; s < 8; s++) {
     const uint32_t wa = w[2 * (s & 3)], wb = w[2 * (s & 3) + 1];
     const uint32_t pa1 = perm(C64, wa, SEL_B0_E_B1_E), pa2 = perm(C64, wa, SEL_B2_E_B3_E);
     const uint32_t pb1 = perm(C64, wb, SEL_B0_E_B1_E), pb2 = perm(C64, wb, SEL_B2_E_B3_E);
-    h8 b;
     if (s < 4) {
-      b = mk_h8(pk_fma(pa1 & 0x640F640Fu, s_lo, c_lo), pk_fma(pa2 & 0x640F640Fu, s_lo, c_lo),
-                pk_fma(pb1 & 0x640F640Fu, s_lo, c_lo), pk_fma(pb2 & 0x640F640Fu, s_lo, c_lo));
+      o.b[s] = mk_h8(pk_fma(pa1 & 0x640F640Fu, s_lo, c_lo), pk_fma(pa2 & 0x640F640Fu, s_lo, c_lo),
+                     pk_fma(pb1 & 0x640F640Fu, s_lo, c_lo), pk_fma(pb2 & 0x640F640Fu, s_lo, c_lo));
     } else {
-      b = mk_h8(pk_fma(pa1 & 0x64F064F0u, s_hi, c_hi), pk_fma(pa2 & 0x64F064F0u, s_hi, c_hi),
-                pk_fma(pb1 & 0x64F064F0u, s_hi, c_hi), pk_fma(pb2 & 0x64F064F0u, s_hi, c_hi));
+      o.b[s] = mk_h8(pk_fma(pa1 & 0x64F064F0u, s_hi, c_hi), pk_fma(pa2 & 0x64F064F0u, s_hi, c_hi),
+                     pk_fma(pb1 & 0x64F064F0u, s_hi, c_hi), pk_fma(pb2 & 0x64F064F0u, s_hi, c_hi));
     }
+  }
+  o.d = f16_bits_to_f32(f.hdr.x);
+  o.dmin = f16_bits_to_f32(f.hdr.x >> 16);
+}
+
+// GEMV step over a decoded K-quant (Q4_K/Q5_K) superblock.  The min term is
+// its own MFMA with B = m(sub-block), so sum_k m(k) x_k = sum_sb m_sb * sum(x in sb).
+template <int XT>
+__device__ __forceinline__ void gemv_kq(const DecKQ& o, const XRow<XT>& xr, int k0, int g, f4& acc) {
+  const h8 bm0 = mk_h8(o.um0, o.um0, o.um0, o.um0), bm1 = mk_h8(o.um1, o.um1, o.um1, o.um1);
+  f4 c = {0, 0, 0, 0}, cm = {0, 0, 0, 0};
+#pragma unroll
+  for (int s = 0; s < 8; s++) {
     const A8<XT> a = load_a8<XT>(xr, k0 + 64 * g + 8 * s);
-    c = mfma_x<XT>(a, b, c);
+    c = mfma_x<XT>(a, o.b[s], c);
     cm = mfma_x<XT>(a, s < 4 ? bm0 : bm1, cm);
   }
-  const float d = f16_bits_to_f32(f.hdr.x), dmin = f16_bits_to_f32(f.hdr.x >> 16);
 #pragma unroll
-  for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(-dmin, cm[r], __builtin_fmaf(d, c[r], acc[r]));
+  for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(-o.dmin, cm[r], __builtin_fmaf(o.d, c[r], acc[r]));
+}
+
+template <int XT>
+__device__ __forceinline__ void compute_q4k(const FragQ4K& f, const XRow<XT>& xr, int k0, int g, f4& acc) {
+  DecKQ o;
+  decode_q4k(f, g, o);
+  gemv_kq<XT>(o, xr, k0, g, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -107,19 +130,17 @@ __device__ __forceinline__ void load_q5k(FragQ5K& f, const uint8_t* sb, int g) {
   f.q0 = ld_u128(sb + 48 + 32 * g);
   f.q1 = ld_u128(sb + 64 + 32 * g);
 }
-template <int XT>
-__device__ __forceinline__ void compute_q5k(const FragQ5K& f, const XRow<XT>& xr, int k0, int g, f4& acc) {
+__device__ __forceinline__ void decode_q5k(const FragQ5K& f, int g, DecKQ& o) {
   uint32_t sc0, m0, sc1, m1;
   scale_min_k4(2 * g, f.hdr.y, f.hdr.z, f.hdr.w, sc0, m0);
   scale_min_k4(2 * g + 1, f.hdr.y, f.hdr.z, f.hdr.w, sc1, m1);
   const h2 s_lo = hsplat((float)sc0), c_lo = hsplat(-1024.0f * (float)sc0);
   const h2 s_hi = hsplat((float)sc1 * 0.0625f), c_hi = hsplat(-64.0f * (float)sc1);
-  const uint32_t um0 = as_u32(hsplat((float)m0)), um1 = as_u32(hsplat((float)m1));
-  const h8 bm0 = mk_h8(um0, um0, um0, um0), bm1 = mk_h8(um1, um1, um1, um1);
+  o.um0 = as_u32(hsplat((float)m0));
+  o.um1 = as_u32(hsplat((float)m1));
   const uint32_t w[8] = {f.q0.x, f.q0.y, f.q0.z, f.q0.w, f.q1.x, f.q1.y, f.q1.z, f.q1.w};
   const uint32_t hb[8] = {f.h0.x, f.h0.y, f.h0.z, f.h0.w, f.h1.x, f.h1.y, f.h1.z, f.h1.w};
   const int rl = (2 * g - 4) & 31, shh = 2 * g + 1;
-  f4 c = {0, 0, 0, 0}, cm = {0, 0, 0, 0};
 #pragma unroll
   for (int s = 0; s < 8; s++) {
     const int i0 = 2 * (s & 3);
@@ -139,14 +160,17 @@ __device__ __forceinline__ void compute_q5k(const FragQ5K& f, const XRow<XT>& xr
         u[2 * e + 1] = pk_fma(perm(hx, wq, SEL_X_B23) & 0x65F065F0u, s_hi, c_hi);
       }
     }
-    const h8 b = mk_h8(u[0], u[1], u[2], u[3]);
-    const A8<XT> a = load_a8<XT>(xr, k0 + 64 * g + 8 * s);
-    c = mfma_x<XT>(a, b, c);
-    cm = mfma_x<XT>(a, s < 4 ? bm0 : bm1, cm);
+    o.b[s] = mk_h8(u[0], u[1], u[2], u[3]);
   }
-  const float d = f16_bits_to_f32(f.hdr.x), dmin = f16_bits_to_f32(f.hdr.x >> 16);
-#pragma unroll
-  for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(-dmin, cm[r], __builtin_fmaf(d, c[r], acc[r]));
+  o.d = f16_bits_to_f32(f.hdr.x);
+  o.dmin = f16_bits_to_f32(f.hdr.x >> 16);
+}
+
+template <int XT>
+__device__ __forceinline__ void compute_q5k(const FragQ5K& f, const XRow<XT>& xr, int k0, int g, f4& acc) {
+  DecKQ o;
+  decode_q5k(f, g, o);
+  gemv_kq<XT>(o, xr, k0, g, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -169,13 +193,20 @@ __device__ __forceinline__ void load_q6k(FragQ6K& f, const uint8_t* sb, int g) {
   f.sc = ld_u64(sb + 192 + 8 * hh);
   f.d = ld_u16(sb + 208);
 }
-template <int XT>
-__device__ __forceinline__ void compute_q6k(const FragQ6K& f, const XRow<XT>& xr, int k0, int g, f4& acc) {
-  const int hh = g >> 1, s = g & 1;
+// MFMA B operands of one Q6_K superblock for this lane: for step st = 2t + e
+// (k = 128hh + 32t + 16s + 8e .. +7), bh[st] = (q-32)*sh and bl[st] = (q-32)*sl.
+struct DecQ6 {
+  h8 bh[8], bl[8];
+  float d;
+};
+__device__ __forceinline__ int q6k_koff(int g, int st) {
+  return 128 * (g >> 1) + 32 * (st >> 1) + 16 * (g & 1) + 8 * (st & 1);
+}
+__device__ __forceinline__ void decode_q6k(const FragQ6K& f, int g, DecQ6& o) {
+  const int s = g & 1;
   const uint32_t qa[4] = {f.qa.x, f.qa.y, f.qa.z, f.qa.w};
   const uint32_t qb[4] = {f.qb.x, f.qb.y, f.qb.z, f.qb.w};
   const uint32_t qh[4] = {f.qh.x, f.qh.y, f.qh.z, f.qh.w};
-  f4 chi = {0, 0, 0, 0}, clo = {0, 0, 0, 0};
 #pragma unroll
   for (int t = 0; t < 4; t++) {
     // scale byte index s + 2t within the 8 scales of this half
@@ -214,14 +245,26 @@ __device__ __forceinline__ void compute_q6k(const FragQ6K& f, const XRow<XT>& xr
         ul[2 * i] = pk_fma(v1, sl_s, sl_c);
         ul[2 * i + 1] = pk_fma(v2, sl_s, sl_c);
       }
-      const A8<XT> a = load_a8<XT>(xr, k0 + 128 * hh + 32 * t + 16 * s + 8 * e);
-      chi = mfma_x<XT>(a, mk_h8(uh[0], uh[1], uh[2], uh[3]), chi);
-      clo = mfma_x<XT>(a, mk_h8(ul[0], ul[1], ul[2], ul[3]), clo);
+      o.bh[2 * t + e] = mk_h8(uh[0], uh[1], uh[2], uh[3]);
+      o.bl[2 * t + e] = mk_h8(ul[0], ul[1], ul[2], ul[3]);
     }
   }
-  const float d = f16_bits_to_f32(f.d);
+  o.d = f16_bits_to_f32(f.d);
+}
+
+template <int XT>
+__device__ __forceinline__ void compute_q6k(const FragQ6K& f, const XRow<XT>& xr, int k0, int g, f4& acc) {
+  DecQ6 o;
+  decode_q6k(f, g, o);
+  f4 chi = {0, 0, 0, 0}, clo = {0, 0, 0, 0};
 #pragma unroll
-  for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(d, __builtin_fmaf(16.0f, chi[r], clo[r]), acc[r]);
+  for (int st = 0; st < 8; st++) {
+    const A8<XT> a = load_a8<XT>(xr, k0 + q6k_koff(g, st));
+    chi = mfma_x<XT>(a, o.bh[st], chi);
+    clo = mfma_x<XT>(a, o.bl[st], clo);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(o.d, __builtin_fmaf(16.0f, chi[r], clo[r]), acc[r]);
 }
 
 // ---------------------------------------------------------------------------

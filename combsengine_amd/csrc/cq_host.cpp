@@ -107,6 +107,14 @@ struct GemvArgs {
   int kc;
   int lds_stride;
 };
+struct GemmArgs {
+  const void* w;
+  const void* x;
+  void* y;
+  long long row_bytes;
+  int M, N, K;
+  int units;
+};
 struct DequantArgs {
   const void* w;
   float* out;
@@ -122,6 +130,7 @@ struct DeviceModule {
   hipModule_t mod = nullptr;
   hipFunction_t gemv[6][2][2] = {};  // [format][x f32][y f16]
   hipFunction_t dequant[6] = {};
+  hipFunction_t gemm[6][2][2] = {};  // K-quant formats only
 };
 DeviceModule g_dev[kMaxDevices];
 
@@ -151,6 +160,16 @@ void load_module(DeviceModule& d, int dev) {
           return;
         }
       }
+    if (block_values(kFormats[fi]) == 256) {
+      for (int xt = 0; xt < 2; xt++)
+        for (int yt = 0; yt < 2; yt++) {
+          snprintf(name, sizeof name, "cq_gemm_%s_x%s_y%s", fn, xt ? "f32" : "f16", yt ? "f16" : "f32");
+          if (hipModuleGetFunction(&d.gemm[fi][xt][yt], d.mod, name) != hipSuccess) {
+            d.err = std::string("missing kernel ") + name;
+            return;
+          }
+        }
+    }
     snprintf(name, sizeof name, "cq_dequant_%s", fn);
     if (hipModuleGetFunction(&d.dequant[fi], d.mod, name) != hipSuccess) {
       d.err = std::string("missing kernel ") + name;
@@ -321,6 +340,31 @@ static cq_status launch_gemv(DeviceModule* dm, const cq_weight* w, const void* x
   return CQ_OK;
 }
 
+// Prefill GEMM (cq_gemm_*, K-quants): workgroups of nw waves x 16 weight rows
+// and 64 (fp16 x) or 32 (fp32 x) activation rows.
+static cq_status launch_gemm(DeviceModule* dm, const cq_weight* w, const void* x, int xt, int64_t m, void* y, int yt,
+                             hipStream_t s) {
+  const int fi = fmt_index(w->format);
+  GemmArgs a;
+  a.w = w->dev;
+  a.x = x;
+  a.y = y;
+  a.row_bytes = (long long)(w->nbytes / (size_t)w->n);
+  a.M = (int)m;
+  a.N = (int)w->n;
+  a.K = (int)w->k;
+  a.units = (int)(w->k / 256);
+  int nw = env_int("COMBS_GEMM_WAVES", 4);
+  if (nw < 4 || nw > 8) nw = 4;  // the activation staging assumes >= 256 threads
+  const int mb = xt ? 32 : 64;
+  const long long gx = (w->n + 16 * nw - 1) / (16 * nw), gy = (m + mb - 1) / mb;
+  if (gx > 0x7fffffffLL || gy > 65535) return fail(CQ_ERR_BAD_SHAPE, "grid too large");
+  void* params[] = {&a};
+  HIP_TRY(hipModuleLaunchKernel(dm->gemm[fi][xt][yt], (unsigned)gx, (unsigned)gy, 1, 64 * nw, 1, 1, 0, s, params,
+                                nullptr));
+  return CQ_OK;
+}
+
 cq_status cq_matmul_path(const cq_weight* w, const void* x, int x_dtype, int64_t m, void* y, int y_dtype, int path,
                          void* stream) {
   if (!w || !x || !y) return fail(CQ_ERR_NULL, "NULL weight, x or y");
@@ -333,7 +377,14 @@ cq_status cq_matmul_path(const cq_weight* w, const void* x, int x_dtype, int64_t
   DeviceModule* dm;
   cq_status st = device_module(&dm);
   if (st != CQ_OK) return st;
-  return launch_gemv(dm, w, x, x_dtype == CQ_F32, m, y, y_dtype == CQ_F16, (hipStream_t)stream);
+  const int xt = x_dtype == CQ_F32, yt = y_dtype == CQ_F16;
+  // Prefill GEMM for m > 16 on K-quants (or when forced); the GEMV kernel
+  // tiles m by 16 otherwise.  Legacy 32-value formats always use the GEMV
+  // kernel.
+  const bool kq = block_values(w->format) == 256;
+  if (kq && (path == CQ_PATH_GEMM || (path == CQ_PATH_AUTO && m > 16)))
+    return launch_gemm(dm, w, x, xt, m, y, yt, (hipStream_t)stream);
+  return launch_gemv(dm, w, x, xt, m, y, yt, (hipStream_t)stream);
 }
 
 cq_status cq_matmul(const cq_weight* w, const void* x, int x_dtype, int64_t m, void* y, int y_dtype, void* stream) {

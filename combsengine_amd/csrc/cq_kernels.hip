@@ -3,8 +3,10 @@
 // hipModuleLoadData.  Kernel names are extern "C" so the host can look them
 // up with hipModuleGetFunction:
 //   cq_gemv_<fmt>_x<f16|f32>_y<f32|f16>   decode GEMV (m-tiles of 16)
+//   cq_gemm_<fmt>_x<f16|f32>_y<f32|f16>   prefill dequant-GEMM (K-quants)
 //   cq_dequant_<fmt>                      bit-exact dequantisation
 #include "cq_gemv.h"
+#include "cq_gemm.h"
 #include "cq_dequant.h"
 
 #define GEMV_KERNEL(NAME, FMT, XT, YT)                                               \
@@ -37,3 +39,17 @@ DEQUANT_KERNEL(q8_0, CQ_Q8_0)
 DEQUANT_KERNEL(q4_k, CQ_Q4_K)
 DEQUANT_KERNEL(q5_k, CQ_Q5_K)
 DEQUANT_KERNEL(q6_k, CQ_Q6_K)
+
+#define GEMM_KERNEL(NAME, FMT, XT, YT)                                               \
+  extern "C" __global__ void __launch_bounds__(512) NAME(const GemmArgs a) {         \
+    gemm_body<FMT, XT, YT>(a);                                                       \
+  }
+#define GEMM_FMT(fname, FMT)                          \
+  GEMM_KERNEL(cq_gemm_##fname##_xf16_yf32, FMT, 0, 0) \
+  GEMM_KERNEL(cq_gemm_##fname##_xf16_yf16, FMT, 0, 1) \
+  GEMM_KERNEL(cq_gemm_##fname##_xf32_yf32, FMT, 1, 0) \
+  GEMM_KERNEL(cq_gemm_##fname##_xf32_yf16, FMT, 1, 1)
+
+GEMM_FMT(q4_k, CQ_Q4_K)
+GEMM_FMT(q5_k, CQ_Q5_K)
+GEMM_FMT(q6_k, CQ_Q6_K)

@@ -154,3 +154,39 @@ def test_gemv_large_and_ragged(cuda, fmt, n, k, m):
     x = O.x_pattern(m, k, 13, 31, 15.0, 16.0).reshape(m, k)
     print(f"{fmt.name} n={n} k={k} m={m}", flush=True)
     O.assert_close(_run(w, x, torch.float16, torch.float32), O.ref_matmul(x, wd), 1e-3, "gemv")
+
+
+KQ = [QuantFormat.Q4K, QuantFormat.Q5K, QuantFormat.Q6K]
+
+
+@pytest.mark.parametrize("fmt", KQ)
+@pytest.mark.parametrize("m", [1, 17, 64, 100, 130])
+def test_gemm_parity(cuda, fmt, m):
+    """Prefill dequant-GEMM (forced for small m too) vs the oracle, fp16/fp32
+    activations, fp32/fp16 outputs, ragged m and n."""
+    import torch
+    n, k = 300, 1024
+    data = synth(fmt, n, k)
+    wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
+    w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
+    x = O.x_pattern(m, k, 11, 29, 14.0, 16.0).reshape(m, k)
+    expect = O.ref_matmul(x, wd)
+    print(f"gemm {fmt.name} m={m}", flush=True)
+    O.assert_close(_run(w, x, torch.float16, torch.float32, path=L.CQ_PATH_GEMM), expect, 1e-3, "x16 y32")
+    O.assert_close(_run(w, x, torch.float32, torch.float16, path=L.CQ_PATH_GEMM), expect, 1e-3, "x32 y16")
+
+
+@pytest.mark.parametrize("fmt", KQ)
+def test_gemm_gaussian_prefill_shape(cuda, fmt):
+    """Quantised N(0, 0.02) weights, N(0, 1) fp16 activations, prefill m=128,
+    checked against a float64 torch matmul of the (bit-exact) GPU dequant."""
+    import torch
+    rng = np.random.default_rng(7 + int(fmt))
+    n, k, m = 1024, 4096, 128
+    data = quantize(fmt, rng.normal(0, 0.02, (n, k)).astype(np.float32))
+    w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
+    wd = torch.from_numpy(dequantize_gpu(fmt, data).reshape(n, k)).cuda().double()
+    x = torch.from_numpy(rng.normal(0, 1, (m, k)).astype(np.float16)).cuda()
+    y = w.matmul_device(x, out_dtype=torch.float32)
+    ref = (x.double() @ wd.t()).cpu().numpy()
+    O.assert_close(y.cpu().numpy(), ref, 1e-3, "gemm m=128")

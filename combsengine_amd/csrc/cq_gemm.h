@@ -30,8 +30,15 @@ struct GemmArgs {
 };
 
 #define GM_KC 256           // K values per step (one superblock)
-#define GM_XP (GM_KC + 8)   // LDS row pitch of the activation chunk (halves)
+#define GM_XP GM_KC         // LDS row pitch of the activation chunk (halves)
 #define GM_XS_REG 8         // 16-byte activation vectors a thread stages per step
+
+// LDS bank swizzle of the activation chunk.  Row r keeps its 16-byte chunk c
+// at position c ^ gm_sw(r).  An MFMA A read is served 32 lanes at a time on
+// gfx950 (16 rows x 2 k-groups whose chunks differ by 8); gm_sw takes 16
+// values whose pairwise XOR never equals 8, so those 32 reads land on 32
+// distinct 16-byte bank groups of the 512-byte LDS row.
+__device__ __forceinline__ int gm_sw(int r) { return (r & 7) | ((r & 8) << 1); }
 
 template <int XT>
 struct GmStage {
@@ -66,13 +73,18 @@ __device__ __forceinline__ void gm_commit(const GmStage<XT>& st, _Float16 (*xh)[
   for (int q = 0; q < GM_XS_REG; q++) {
     const int i = threadIdx.x + q * blockDim.x;
     if (q * (int)blockDim.x >= total) break;  // later slots are empty for every thread
-    float f[8];
     h8 vh, vl;
+    float sum;
     if (!XT) {
       vh = __builtin_bit_cast(h8, st.v[q][0]);
-#pragma unroll
-      for (int e = 0; e < 8; e++) f[e] = (float)vh[e];
+      // exact products by 1.0, f32 accumulation (v_dot2_f32_f16)
+      const h2 one = {1, 1};
+      sum = __builtin_amdgcn_fdot2(as_h2(st.v[q][0].x), one, 0.0f, false);
+      sum = __builtin_amdgcn_fdot2(as_h2(st.v[q][0].y), one, sum, false);
+      sum = __builtin_amdgcn_fdot2(as_h2(st.v[q][0].z), one, sum, false);
+      sum = __builtin_amdgcn_fdot2(as_h2(st.v[q][0].w), one, sum, false);
     } else {
+      float f[8];
       __builtin_memcpy(f, &st.v[q][0], 16);
       __builtin_memcpy(f + 4, &st.v[q][XT], 16);
 #pragma unroll
@@ -80,14 +92,15 @@ __device__ __forceinline__ void gm_commit(const GmStage<XT>& st, _Float16 (*xh)[
         vh[e] = (_Float16)f[e];
         vl[e] = (_Float16)(f[e] - (float)vh[e]);
       }
+      sum = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
     }
-    float sum = ((f[0] + f[1]) + (f[2] + f[3])) + ((f[4] + f[5]) + (f[6] + f[7]));
     sum += __shfl_xor(sum, 1);
     sum += __shfl_xor(sum, 2);
     if (i < total) {
       const int r = i >> 5, v = i & 31;
-      *(h8*)&xh[r][8 * v] = vh;
-      if (XT) *(h8*)&xl[r][8 * v] = vl;
+      const int pv = 8 * (v ^ gm_sw(r & 15));
+      *(h8*)&xh[r][pv] = vh;
+      if (XT) *(h8*)&xl[r][pv] = vl;
       if ((v & 3) == 0) {
         const _Float16 hi = (_Float16)sum;
         xsum[r][2 * (v >> 2)] = hi;
@@ -129,6 +142,14 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
   f4 acc[MT];
 #pragma unroll
   for (int t = 0; t < MT; t++) acc[t] = f4{0, 0, 0, 0};
+  // swizzled column (halves) of this lane's 8 A values for each MFMA step
+  const int swj = gm_sw(j);
+  int acol[8];
+#pragma unroll
+  for (int s = 0; s < 8; s++) {
+    const int c = (FMT == CQ_Q6_K) ? q6k_koff(g, s) / 8 : 8 * g + s;
+    acol[s] = 8 * (c ^ swj);
+  }
 
   GmStage<XT> st;
   gm_issue<XT, MB>(a, st, m0, 0);
@@ -146,46 +167,56 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
     }
     const _Float16(*xb)[GM_XP] = xh[b];
     const _Float16(*xbl)[GM_XP] = xl[XT ? b : 0];
+    // Steps outer, activation tiles inner: the MT accumulation chains are
+    // independent, so consecutive MFMAs never wait on each other.
     if constexpr (FMT == CQ_Q6_K) {
       DecQ6 o;
       decode_q6k(cur, g, o);
+      f4 chi[MT], clo[MT];
 #pragma unroll
-      for (int t = 0; t < MT; t++) {
-        f4 chi = {0, 0, 0, 0}, clo = {0, 0, 0, 0};
+      for (int t = 0; t < MT; t++) chi[t] = clo[t] = f4{0, 0, 0, 0};
 #pragma unroll
-        for (int s = 0; s < 8; s++) {
-          const int ko = q6k_koff(g, s);
-          const h8 av = *(const h8*)&xb[16 * t + j][ko];
-          chi = mfma(av, o.bh[s], chi);
-          clo = mfma(av, o.bl[s], clo);
+      for (int s = 0; s < 8; s++) {
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+          const h8 av = *(const h8*)&xb[16 * t + j][acol[s]];
+          chi[t] = mfma(av, o.bh[s], chi[t]);
+          clo[t] = mfma(av, o.bl[s], clo[t]);
           if (XT) {
-            const h8 al = *(const h8*)&xbl[16 * t + j][ko];
-            chi = mfma(al, o.bh[s], chi);
-            clo = mfma(al, o.bl[s], clo);
+            const h8 al = *(const h8*)&xbl[16 * t + j][acol[s]];
+            chi[t] = mfma(al, o.bh[s], chi[t]);
+            clo[t] = mfma(al, o.bl[s], clo[t]);
           }
         }
-#pragma unroll
-        for (int r = 0; r < 4; r++) acc[t][r] = __builtin_fmaf(o.d, __builtin_fmaf(16.0f, chi[r], clo[r]), acc[t][r]);
       }
+#pragma unroll
+      for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          acc[t][r] = __builtin_fmaf(o.d, __builtin_fmaf(16.0f, chi[t][r], clo[t][r]), acc[t][r]);
     } else {
       DecKQ o;
       if constexpr (FMT == CQ_Q4_K) decode_q4k(cur, g, o);
       else decode_q5k(cur, g, o);
       const h8 bmin = kq_min_operand(cur.hdr, g);
       const h8 zero = {0, 0, 0, 0, 0, 0, 0, 0};
+      f4 c[MT];
+#pragma unroll
+      for (int t = 0; t < MT; t++) c[t] = f4{0, 0, 0, 0};
+#pragma unroll
+      for (int s = 0; s < 8; s++) {
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+          c[t] = mfma(*(const h8*)&xb[16 * t + j][acol[s]], o.b[s], c[t]);
+          if (XT) c[t] = mfma(*(const h8*)&xbl[16 * t + j][acol[s]], o.b[s], c[t]);
+        }
+      }
 #pragma unroll
       for (int t = 0; t < MT; t++) {
-        f4 c = {0, 0, 0, 0};
-#pragma unroll
-        for (int s = 0; s < 8; s++) {
-          const int ko = 64 * g + 8 * s;
-          c = mfma(*(const h8*)&xb[16 * t + j][ko], o.b[s], c);
-          if (XT) c = mfma(*(const h8*)&xbl[16 * t + j][ko], o.b[s], c);
-        }
         const h8 as = g < 2 ? *(const h8*)&xsum[b][16 * t + j][8 * g] : zero;
         const f4 cm = mfma(as, bmin, f4{0, 0, 0, 0});
 #pragma unroll
-        for (int r = 0; r < 4; r++) acc[t][r] = __builtin_fmaf(-o.dmin, cm[r], __builtin_fmaf(o.d, c[r], acc[t][r]));
+        for (int r = 0; r < 4; r++) acc[t][r] = __builtin_fmaf(-o.dmin, cm[r], __builtin_fmaf(o.d, c[t][r], acc[t][r]));
       }
     }
     if (more) {

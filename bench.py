@@ -2,19 +2,23 @@
 
 Headline (BASELINE.json metric "Q4_K decode GEMV HBM GB/s (% of peak)"):
 one step = one decode token's Q4_K projections at Llama-3-8B shapes, batch 1:
-W_gate-shape [14336 x 4096] and W_down-shape [4096 x 14336] (the two K-quant
-projection shapes of config 3), x fp16 N(0, 1), y fp32.  Weights are
-N(0, 0.02) quantised to Q4_K from a seed and replicated into a weight pool of
->= 1 GiB of distinct device buffers that the steps rotate through, so every
-launch streams its weight from HBM, not from the 256 MB Infinity Cache.
+a [14336 x 4096] (gate/up) and a [4096 x 14336] (down) GEMV, the two K-quant
+projection shapes of BASELINE config 3; x fp16 N(0, 1), y fp32.  Weights are
+N(0, 0.02) quantised to Q4_K from a seed and replicated into a pool of
+>= 1.25 GiB of distinct device buffers that the steps rotate through, so each
+launch streams its weight from HBM rather than the 256 MB Infinity Cache.
 
-value = algorithmic bytes (GGUF-native weight bytes + x + y) per step x steps
-        / wall time of the timed steps (inputs resident in HBM).
+The K timed steps are captured once into a HIP graph (torch.cuda.CUDAGraph
+over the library's hipModuleLaunchKernel calls) and replayed, so the number
+measures the kernels back to back rather than Python's launch overhead.
+
+value = algorithmic bytes (GGUF-native weight bytes + x + y) of K steps
+        / device time of the K steps (HIP events around the graph replay).
 
 Also reported: the roofline of the dominant kernel (cq_gemv_q4_k_xf16_yf32)
-from per-launch HIP events, secondary numbers (lm_head Q6_K, batch 4/16,
-prefill TFLOP/s), and the reference CPU path (dequantise once, dense f32
-GEMV per call) timed on this host as cpu_baseline.
+from graphs of single-shape launches, prefill dequant-GEMM TFLOP/s (config 4),
+lm_head Q6_K and batch 4/16, and the reference CPU path (dequantise once,
+dense f32 GEMV per call) timed on this host as cpu_baseline.
 """
 import argparse
 import json
@@ -34,6 +38,7 @@ def algo_bytes(wbytes, m, k, n, xbytes=2, ybytes=4):
 
 
 def make_pool(fmt, n, k, pool_bytes, seed):
+    """One seeded quantised weight, replicated into distinct device buffers."""
     import numpy as np
     import torch
     from combsengine_amd import QuantWeight, quantize
@@ -41,25 +46,44 @@ def make_pool(fmt, n, k, pool_bytes, seed):
     data = np.frombuffer(quantize(fmt, rng.normal(0, 0.02, (n, k)).astype(np.float32)), np.uint8)
     base = torch.from_numpy(data.copy()).cuda()
     count = max(1, int(pool_bytes // data.size))
-    pool = []
-    for i in range(count):
-        t = base if i == 0 else base.clone()
-        pool.append(QuantWeight.from_device(fmt, t, n, k))
+    pool = [QuantWeight.from_device(fmt, base if i == 0 else base.clone(), n, k) for i in range(count)]
     return pool, data
 
 
-def time_launch_durations(fn, launches):
-    """Mean device duration of single launches, bracketed by HIP events on the
-    stream the kernel runs on (torch's current stream)."""
+def graph_time_us(launch, count, reps=3):
+    """Capture `count` launches (launch(i)) in one HIP graph; return the
+    device time per launch (us), best of `reps` replays."""
     import torch
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(launches)]
-    for i, (a, b) in enumerate(evs):
-        a.record()
-        fn(i)
-        b.record()
+    launch(0)  # make sure the library and modules are loaded outside capture
     torch.cuda.synchronize()
-    d = sorted(a.elapsed_time(b) * 1e3 for a, b in evs)  # us
-    return sum(d) / len(d), d[len(d) // 10], d[len(d) // 2], d[(9 * len(d)) // 10]
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for i in range(count):
+                launch(i)
+    torch.cuda.current_stream().wait_stream(s)
+    g.replay()
+    torch.cuda.synchronize()
+    best = None
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        t = a.elapsed_time(b) * 1e3 / count
+        best = t if best is None else min(best, t)
+    return best, g
+
+
+def load_traffic():
+    p = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(p):
+        with open(p) as f:
+            return json.load(f)
+    return {}
 
 
 def cpu_baseline(seconds=6.0):
@@ -99,6 +123,43 @@ def cpu_baseline(seconds=6.0):
     }
 
 
+def secondary(dev):
+    """Prefill dequant-GEMM (config 4), lm_head Q6_K and batch 4/16 GEMV."""
+    import numpy as np
+    import torch
+    from combsengine_amd import QuantFormat
+    out = {}
+    rng = np.random.default_rng(9)
+    # prefill: M in {128, 512, 2048} x Q4_K [14336 x 4096] and Q6_K [4096 x 14336], fp16 out
+    for fmt, n, k in ((QuantFormat.Q4K, 14336, 4096), (QuantFormat.Q6K, 4096, 14336)):
+        pool, data = make_pool(fmt, n, k, 0.3 * (1 << 30), seed=300 + int(fmt))
+        for m in (128, 512, 2048):
+            x = torch.from_numpy(rng.normal(0, 1, (m, k)).astype(np.float16)).to(dev)
+            y = torch.empty((m, n), dtype=torch.float16, device=dev)
+            us, _ = graph_time_us(lambda i: pool[i % len(pool)].matmul_into(x, y), 10 if m < 2048 else 4)
+            fl = 2.0 * m * n * k
+            out[f"prefill_{fmt.name}_{n}x{k}_m{m}"] = {"us": round(us, 2), "TFLOPs": round(fl / us / 1e6, 1),
+                                                      "frac_fp16_peak": round(fl / us / 1e6 / FP16_PEAK_TFLOPS, 4)}
+        del pool
+    # lm_head Q6_K [128256 x 4096] (431 MB: larger than the Infinity Cache)
+    pool, data = make_pool(QuantFormat.Q6K, 128256, 4096, 2 * 431e6, seed=77)
+    x = torch.from_numpy(rng.normal(0, 1, (1, 4096)).astype(np.float16)).to(dev)
+    y = torch.empty((1, 128256), dtype=torch.float32, device=dev)
+    us, _ = graph_time_us(lambda i: pool[i % len(pool)].matmul_into(x, y), 8)
+    b = algo_bytes(data.size, 1, 4096, 128256)
+    out["lm_head_q6_k_m1"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1)}
+    del pool
+    # decode batch 4 / 16 on the gate shape
+    pool, data = make_pool(QuantFormat.Q4K, 14336, 4096, 0.6 * (1 << 30), seed=1000)
+    for m in (4, 16):
+        x = torch.from_numpy(rng.normal(0, 1, (m, 4096)).astype(np.float16)).to(dev)
+        y = torch.empty((m, 14336), dtype=torch.float32, device=dev)
+        us, _ = graph_time_us(lambda i: pool[i % len(pool)].matmul_into(x, y), 2 * len(pool))
+        b = algo_bytes(data.size, m, 4096, 14336)
+        out[f"q4_k_14336x4096_m{m}"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1)}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -109,8 +170,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; the multi-GPU sharding is design-only "
-                          "(output-row split, see DESIGN.md)", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding of the quantized linear "
+                          "layer is design-only (output-row split, see DESIGN.md)", "n_gpus": args.gpus}))
         sys.exit(2)
 
     import numpy as np
@@ -122,9 +183,8 @@ def main():
     fmt = QuantFormat.Q4K
     shapes = [(14336, 4096), (4096, 14336)]
     pools, sizes = [], []
-    per_pool = args.pool_gib * (1 << 30) / len(shapes)
     for si, (n, k) in enumerate(shapes):
-        p, data = make_pool(fmt, n, k, per_pool, seed=1000 + si)
+        p, data = make_pool(fmt, n, k, args.pool_gib * (1 << 30) / len(shapes), seed=1000 + si)
         pools.append(p)
         sizes.append(data.size)
     P = min(len(p) for p in pools)
@@ -140,85 +200,52 @@ def main():
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    for i in range(args.steps):
-        step(i)
-    ev1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_total = ev0.elapsed_time(ev1)
+    # the K timed steps, captured once and replayed (timing brackets the replay)
+    t_cap = time.perf_counter()
+    us_per_step, graph = graph_time_us(step, args.steps, reps=1)
+    wall = time.perf_counter() - t_cap
+    ms_total = us_per_step * args.steps / 1e3
     step_bytes = sum(algo_bytes(sz, 1, k, n) for sz, (n, k) in zip(sizes, shapes))
     value = step_bytes * args.steps / (ms_total / 1e3) / 1e9
 
-    # Dominant kernel: per-launch duration with HIP events, both shapes.
-    launch = {}
-    tot_b, tot_us = 0.0, 0.0
+    # Dominant kernel: launches of one shape back to back in a graph.
+    launch, tot_b, tot_us = {}, 0.0, 0.0
+    traffic = load_traffic().get("cq_gemv_q4_k_xf16_yf32", {})
     for s, (n, k) in enumerate(shapes):
-        mean, p10, p50, p90 = time_launch_durations(lambda i, s=s: pools[s][i % P].matmul_into(xs[s], ys[s]),
-                                                     max(4 * P, 200))
+        us, _ = graph_time_us(lambda i, s=s: pools[s][i % P].matmul_into(xs[s], ys[s]), 4 * P)
         b = algo_bytes(sizes[s], 1, k, n)
-        launch[f"{n}x{k}"] = {"us_mean": round(mean, 3), "us_p10": round(p10, 3), "us_p50": round(p50, 3),
-                              "us_p90": round(p90, 3), "GBps": round(b / mean / 1e3, 1),
-                              "frac": round(b / mean / 1e3 / HBM_PEAK_GBS, 4)}
+        launch[f"{n}x{k}"] = {"us": round(us, 3), "GBps": round(b / us / 1e3, 1),
+                              "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
         tot_b += b
-        tot_us += mean
+        tot_us += us
     achieved = tot_b / tot_us / 1e3
+    t_bytes = [traffic.get(f"{n}x{k}") for (n, k) in shapes]
+    traffic_val = round(sum(t_bytes) / len(t_bytes)) if all(t_bytes) else None
 
-    extra = {}
-    if not args.no_extra:
-        extra = secondary(dev)
+    extra = {} if args.no_extra else secondary(dev)
+    prefill = {k: v for k, v in extra.items() if k.startswith("prefill_")}
+    best_prefill = max((v["TFLOPs"] for v in prefill.values()), default=None)
 
     line = {
         "metric": "Q4_K decode GEMV HBM GB/s (% of peak); prefill dequant-GEMM TFLOP/s",
         "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_total / args.steps, 5), "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "q4_k weights, f16 x, f32 accumulate/out", "data": "synthetic",
-        "config": {"workload": "Q4_K decode GEMV, Llama-3-8B shapes [14336x4096]+[4096x14336], batch 1, "
-                               f"weight pool {P} x {len(shapes)} buffers ({P * sum(sizes) / 2**30:.2f} GiB)",
+        "vs_baseline": None, "dtype": "q4_k", "data": "synthetic",
+        "config": {"workload": "Q4_K decode GEMV, Llama-3-8B shapes [14336x4096]+[4096x14336], batch 1, x f16, "
+                               f"y f32; weight pool {P} x {len(shapes)} buffers ({P * sum(sizes) / 2**30:.2f} GiB)",
                    "global_batch": 1, "parallelism": "none (1 GPU)"},
         "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
         "roofline": {"bound": "hbm", "kernel": "cq_gemv_q4_k_xf16_yf32", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "algorithmic_bytes_per_launch": {f"{n}x{k}": algo_bytes(sz, 1, k, n)
-                                                                       for sz, (n, k) in zip(sizes, shapes)},
-                     "launches": launch},
-        "wall_s_timed": round(wall, 3),
+                     "traffic": traffic_val,
+                     "algorithmic_bytes_per_launch": round(tot_b / len(shapes)), "launches": launch},
+        "prefill_TFLOPs_best": best_prefill,
+        "wall_s_capture_and_replay": round(wall, 3),
         "secondary": extra,
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)
-
-
-def secondary(dev):
-    """lm_head Q6_K GEMV, batch 4/16 Q4_K, and prefill M=128/512 TFLOP/s."""
-    import numpy as np
-    import torch
-    from combsengine_amd import QuantFormat
-    out = {}
-    rng = np.random.default_rng(9)
-    # lm_head Q6_K [128256 x 4096] (431 MB: larger than the Infinity Cache)
-    pool, data = make_pool(QuantFormat.Q6K, 128256, 4096, 2 * 431e6, seed=77)
-    x = torch.from_numpy(rng.normal(0, 1, (1, 4096)).astype(np.float16)).to(dev)
-    y = torch.empty((1, 128256), dtype=torch.float32, device=dev)
-    mean, p10, p50, p90 = time_launch_durations(lambda i: pool[i % len(pool)].matmul_into(x, y), 40)
-    b = algo_bytes(data.size, 1, 4096, 128256)
-    out["lm_head_q6_k_m1"] = {"us": round(mean, 2), "GBps": round(b / mean / 1e3, 1)}
-    del pool
-    # batch 4 / 16 and prefill on the gate shape
-    pool, data = make_pool(QuantFormat.Q4K, 14336, 4096, 0.6 * (1 << 30), seed=1000)
-    for m in (4, 16, 128, 512):
-        x = torch.from_numpy(rng.normal(0, 1, (m, 4096)).astype(np.float16)).to(dev)
-        y = torch.empty((m, 14336), dtype=torch.float16 if m > 16 else torch.float32, device=dev)
-        reps = 40 if m <= 16 else 10
-        mean, p10, p50, p90 = time_launch_durations(lambda i: pool[i % len(pool)].matmul_into(x, y), reps)
-        b = algo_bytes(data.size, m, 4096, 14336, ybytes=2 if m > 16 else 4)
-        fl = 2.0 * m * 4096 * 14336
-        out[f"q4_k_14336x4096_m{m}"] = {"us": round(mean, 2), "GBps": round(b / mean / 1e3, 1),
-                                        "TFLOPs": round(fl / mean / 1e6, 2)}
-    return out
 
 
 if __name__ == "__main__":

@@ -115,6 +115,9 @@ class QuantWeight:
         is not a block multiple."""
         fmt = QuantFormat(fmt)
         buf = np.frombuffer(bytes(data), np.uint8) if not isinstance(data, np.ndarray) else np.ascontiguousarray(data, np.uint8)
+        # shape rules first (no device work on a bad shape, qmatmul.rs:1326-1335)
+        if buf.size != tensor_byte_size(fmt, n_out, k):
+            raise BadShape(f"{fmt.name.lower()} weight", [n_out, k], [buf.size])
         out = ctypes.c_void_p()
         s = stream if stream is not None else _stream_ptr()
         st = L.lib().cq_weight_create(int(fmt), buf.ctypes.data, buf.size, n_out, k, s, ctypes.byref(out))
@@ -162,6 +165,8 @@ class QuantWeight:
     def matmul_into(self, x, y, path: int = L.CQ_PATH_AUTO, stream=None):
         """Launch y[m, n] = x[m, k] . W^T on the current (or given) stream.
         x: CUDA fp16/fp32 contiguous [m, k]; y: CUDA fp32/fp16 contiguous [m, n]."""
+        if not (x.is_cuda and y.is_cuda) or x.device != y.device:
+            raise ModelError("x and y must be device tensors on the weight's device")
         if x.dim() != 2 or x.shape[1] != self._k or not x.is_contiguous():
             raise BadShape(f"{self.format.name.lower()} matmul input", [-1, self._k], list(x.shape))
         m = x.shape[0]
@@ -240,7 +245,8 @@ class Linear:
 
     def forward(self, x, bias=None):
         if self.dense is not None:
-            out = x @ self.dense.t().to(x.dtype)
+            # fp32 accumulation, output in the activation dtype
+            out = (x.float() @ self.dense.t().float()).to(x.dtype)
         else:
             out = self.quant.forward(x)
         if bias is not None:

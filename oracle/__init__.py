@@ -147,11 +147,6 @@ def synth_q4_0(n_blocks: int) -> bytes:
     return out.tobytes()
 
 
-def _f32(v):
-    # The reference computes the scale expression in f32 before f16::from_f32.
-    return float(np.float32(v))
-
-
 def synth_q4_k(n_sb: int) -> bytes:
     """qmatmul.rs:1795-1805."""
     parts = []

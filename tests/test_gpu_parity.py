@@ -190,3 +190,39 @@ def test_gemm_gaussian_prefill_shape(cuda, fmt):
     y = w.matmul_device(x, out_dtype=torch.float32)
     ref = (x.double() @ wd.t()).cpu().numpy()
     O.assert_close(y.cpu().numpy(), ref, 1e-3, "gemm m=128")
+
+
+def test_graph_capture_replays(cuda):
+    """cq_matmul launches captured into a HIP graph replay correctly, with
+    eager work and synchronisations between replays (no memset nodes: the
+    library records none)."""
+    import torch
+    fmt, n, k = QuantFormat.Q4K, 512, 4096
+    rng = np.random.default_rng(3)
+    data = quantize(fmt, rng.normal(0, 0.02, (n, k)).astype(np.float32))
+    w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
+    x = torch.from_numpy(rng.normal(0, 1, (1, k)).astype(np.float16)).cuda()
+    xp = torch.from_numpy(rng.normal(0, 1, (64, k)).astype(np.float16)).cuda()
+    y = torch.empty((1, n), dtype=torch.float32, device="cuda")
+    yp = torch.empty((64, n), dtype=torch.float16, device="cuda")
+    w.matmul_into(x, y)
+    w.matmul_into(xp, yp)
+    torch.cuda.synchronize()
+    ref, refp = y.clone(), yp.clone()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            w.matmul_into(x, y)
+            w.matmul_into(xp, yp)
+    torch.cuda.current_stream().wait_stream(s)
+    for rep in range(4):
+        y.fill_(float("nan"))
+        yp.fill_(float("nan"))
+        _ = (xp.float() @ xp.float().t()).sum()  # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref), rep
+        assert torch.equal(yp, refp), rep

@@ -21,7 +21,10 @@ SO = os.path.join(LIBDIR, "libcombs_qlinear.so")
 
 HIPCC_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17",
                # packed fp32 ops off (the compiler must not emit v_pk_*_f32)
-               "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+               "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+               # keep MFMA operands/results in VGPRs (no AGPR copies around the
+               # fp32 epilogues that scale each superblock's MFMA result)
+               "-mllvm", "-amdgpu-mfma-vgpr-form=1"]
 
 
 def _run(cmd, verbose):

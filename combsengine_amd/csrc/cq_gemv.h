@@ -67,30 +67,51 @@ struct DecKQ {
   uint32_t um0, um1;
   float d, dmin;
 };
-__device__ __forceinline__ void decode_q4k(const FragQ4K& f, int g, DecKQ& o) {
+// Per-lane scale constants of a K-quant superblock: the lane's two
+// sub-blocks 2g (low nibbles) and 2g+1 (high nibbles, seen as 16*q).
+struct KQScale {
+  h2 s_lo, c_lo, s_hi, c_hi;
+  uint32_t um0, um1;
+  float d, dmin;
+};
+__device__ __forceinline__ KQScale kq_scale(const u4v& hdr, int g) {
   uint32_t sc0, m0, sc1, m1;
-  scale_min_k4(2 * g, f.hdr.y, f.hdr.z, f.hdr.w, sc0, m0);
-  scale_min_k4(2 * g + 1, f.hdr.y, f.hdr.z, f.hdr.w, sc1, m1);
-  const h2 s_lo = hsplat((float)sc0), c_lo = hsplat(-1024.0f * (float)sc0);
-  const h2 s_hi = hsplat((float)sc1 * 0.0625f), c_hi = hsplat(-64.0f * (float)sc1);
-  o.um0 = as_u32(hsplat((float)m0));
-  o.um1 = as_u32(hsplat((float)m1));
+  scale_min_k4(2 * g, hdr.y, hdr.z, hdr.w, sc0, m0);
+  scale_min_k4(2 * g + 1, hdr.y, hdr.z, hdr.w, sc1, m1);
+  KQScale k;
+  k.s_lo = hsplat((float)sc0);
+  k.c_lo = hsplat(-1024.0f * (float)sc0);
+  k.s_hi = hsplat((float)sc1 * 0.0625f);
+  k.c_hi = hsplat(-64.0f * (float)sc1);
+  k.um0 = as_u32(hsplat((float)m0));
+  k.um1 = as_u32(hsplat((float)m1));
+  k.d = f16_bits_to_f32(hdr.x);
+  k.dmin = f16_bits_to_f32(hdr.x >> 16);
+  return k;
+}
+// B operand of MFMA step s (k = 64g + 8s .. +7) of a Q4_K superblock.
+__device__ __forceinline__ h8 q4k_b(const FragQ4K& f, const KQScale& k, int s) {
   const uint32_t w[8] = {f.q0.x, f.q0.y, f.q0.z, f.q0.w, f.q1.x, f.q1.y, f.q1.z, f.q1.w};
+  const uint32_t wa = w[2 * (s & 3)], wb = w[2 * (s & 3) + 1];
+  const uint32_t pa1 = perm(C64, wa, SEL_B0_E_B1_E), pa2 = perm(C64, wa, SEL_B2_E_B3_E);
+  const uint32_t pb1 = perm(C64, wb, SEL_B0_E_B1_E), pb2 = perm(C64, wb, SEL_B2_E_B3_E);
+  if (s < 4)
+    return mk_h8(pk_fma(pa1 & 0x640F640Fu, k.s_lo, k.c_lo), pk_fma(pa2 & 0x640F640Fu, k.s_lo, k.c_lo),
+                 pk_fma(pb1 & 0x640F640Fu, k.s_lo, k.c_lo), pk_fma(pb2 & 0x640F640Fu, k.s_lo, k.c_lo));
+  return mk_h8(pk_fma(pa1 & 0x64F064F0u, k.s_hi, k.c_hi), pk_fma(pa2 & 0x64F064F0u, k.s_hi, k.c_hi),
+               pk_fma(pb1 & 0x64F064F0u, k.s_hi, k.c_hi), pk_fma(pb2 & 0x64F064F0u, k.s_hi, k.c_hi));
+}
+__device__ __forceinline__ void kq_finish(const KQScale& k, DecKQ& o) {
+  o.um0 = k.um0;
+  o.um1 = k.um1;
+  o.d = k.d;
+  o.dmin = k.dmin;
+}
+__device__ __forceinline__ void decode_q4k(const FragQ4K& f, int g, DecKQ& o) {
+  const KQScale k = kq_scale(f.hdr, g);
 #pragma unroll
-  for (int s = 0; s < 8; s++) {
-    const uint32_t wa = w[2 * (s & 3)], wb = w[2 * (s & 3) + 1];
-    const uint32_t pa1 = perm(C64, wa, SEL_B0_E_B1_E), pa2 = perm(C64, wa, SEL_B2_E_B3_E);
-    const uint32_t pb1 = perm(C64, wb, SEL_B0_E_B1_E), pb2 = perm(C64, wb, SEL_B2_E_B3_E);
-    if (s < 4) {
-      o.b[s] = mk_h8(pk_fma(pa1 & 0x640F640Fu, s_lo, c_lo), pk_fma(pa2 & 0x640F640Fu, s_lo, c_lo),
-                     pk_fma(pb1 & 0x640F640Fu, s_lo, c_lo), pk_fma(pb2 & 0x640F640Fu, s_lo, c_lo));
-    } else {
-      o.b[s] = mk_h8(pk_fma(pa1 & 0x64F064F0u, s_hi, c_hi), pk_fma(pa2 & 0x64F064F0u, s_hi, c_hi),
-                     pk_fma(pb1 & 0x64F064F0u, s_hi, c_hi), pk_fma(pb2 & 0x64F064F0u, s_hi, c_hi));
-    }
-  }
-  o.d = f16_bits_to_f32(f.hdr.x);
-  o.dmin = f16_bits_to_f32(f.hdr.x >> 16);
+  for (int s = 0; s < 8; s++) o.b[s] = q4k_b(f, k, s);
+  kq_finish(k, o);
 }
 
 // GEMV step over a decoded K-quant (Q4_K/Q5_K) superblock.  The min term is
@@ -130,40 +151,35 @@ __device__ __forceinline__ void load_q5k(FragQ5K& f, const uint8_t* sb, int g) {
   f.q0 = ld_u128(sb + 48 + 32 * g);
   f.q1 = ld_u128(sb + 64 + 32 * g);
 }
-__device__ __forceinline__ void decode_q5k(const FragQ5K& f, int g, DecKQ& o) {
-  uint32_t sc0, m0, sc1, m1;
-  scale_min_k4(2 * g, f.hdr.y, f.hdr.z, f.hdr.w, sc0, m0);
-  scale_min_k4(2 * g + 1, f.hdr.y, f.hdr.z, f.hdr.w, sc1, m1);
-  const h2 s_lo = hsplat((float)sc0), c_lo = hsplat(-1024.0f * (float)sc0);
-  const h2 s_hi = hsplat((float)sc1 * 0.0625f), c_hi = hsplat(-64.0f * (float)sc1);
-  o.um0 = as_u32(hsplat((float)m0));
-  o.um1 = as_u32(hsplat((float)m1));
+// B operand of MFMA step s of a Q5_K superblock (same k mapping as Q4_K).
+__device__ __forceinline__ h8 q5k_b(const FragQ5K& f, const KQScale& k, int g, int s) {
   const uint32_t w[8] = {f.q0.x, f.q0.y, f.q0.z, f.q0.w, f.q1.x, f.q1.y, f.q1.z, f.q1.w};
   const uint32_t hb[8] = {f.h0.x, f.h0.y, f.h0.z, f.h0.w, f.h1.x, f.h1.y, f.h1.z, f.h1.w};
   const int rl = (2 * g - 4) & 31, shh = 2 * g + 1;
+  const int i0 = 2 * (s & 3);
+  uint32_t u[4];
 #pragma unroll
-  for (int s = 0; s < 8; s++) {
-    const int i0 = 2 * (s & 3);
-    uint32_t u[4];
-#pragma unroll
-    for (int e = 0; e < 2; e++) {
-      const uint32_t wq = w[i0 + e], hq = hb[i0 + e];
-      if (s < 4) {
-        // rotate bit 2g of each qh byte to bit 4 and insert it above the low nibble
-        const uint32_t z = bfi(0x10101010u, rotr(hq, rl), wq);
-        u[2 * e] = pk_fma(perm(C64, z, SEL_B0_E_B1_E) & 0x641F641Fu, s_lo, c_lo);
-        u[2 * e + 1] = pk_fma(perm(C64, z, SEL_B2_E_B3_E) & 0x641F641Fu, s_lo, c_lo);
-      } else {
-        // high nibble at bits 4-7 of the half, bit 2g+1 of qh at bit 8 under 0x64
-        const uint32_t hx = ((hq >> shh) & 0x01010101u) | C64;
-        u[2 * e] = pk_fma(perm(hx, wq, SEL_X_B01) & 0x65F065F0u, s_hi, c_hi);
-        u[2 * e + 1] = pk_fma(perm(hx, wq, SEL_X_B23) & 0x65F065F0u, s_hi, c_hi);
-      }
+  for (int e = 0; e < 2; e++) {
+    const uint32_t wq = w[i0 + e], hq = hb[i0 + e];
+    if (s < 4) {
+      // rotate bit 2g of each qh byte to bit 4 and insert it above the low nibble
+      const uint32_t z = bfi(0x10101010u, rotr(hq, rl), wq);
+      u[2 * e] = pk_fma(perm(C64, z, SEL_B0_E_B1_E) & 0x641F641Fu, k.s_lo, k.c_lo);
+      u[2 * e + 1] = pk_fma(perm(C64, z, SEL_B2_E_B3_E) & 0x641F641Fu, k.s_lo, k.c_lo);
+    } else {
+      // high nibble at bits 4-7 of the half, bit 2g+1 of qh at bit 8 under 0x64
+      const uint32_t hx = ((hq >> shh) & 0x01010101u) | C64;
+      u[2 * e] = pk_fma(perm(hx, wq, SEL_X_B01) & 0x65F065F0u, k.s_hi, k.c_hi);
+      u[2 * e + 1] = pk_fma(perm(hx, wq, SEL_X_B23) & 0x65F065F0u, k.s_hi, k.c_hi);
     }
-    o.b[s] = mk_h8(u[0], u[1], u[2], u[3]);
   }
-  o.d = f16_bits_to_f32(f.hdr.x);
-  o.dmin = f16_bits_to_f32(f.hdr.x >> 16);
+  return mk_h8(u[0], u[1], u[2], u[3]);
+}
+__device__ __forceinline__ void decode_q5k(const FragQ5K& f, int g, DecKQ& o) {
+  const KQScale k = kq_scale(f.hdr, g);
+#pragma unroll
+  for (int s = 0; s < 8; s++) o.b[s] = q5k_b(f, k, g, s);
+  kq_finish(k, o);
 }
 
 template <int XT>
@@ -202,53 +218,52 @@ struct DecQ6 {
 __device__ __forceinline__ int q6k_koff(int g, int st) {
   return 128 * (g >> 1) + 32 * (st >> 1) + 16 * (g & 1) + 8 * (st & 1);
 }
-__device__ __forceinline__ void decode_q6k(const FragQ6K& f, int g, DecQ6& o) {
-  const int s = g & 1;
+// B operands of MFMA step st = 2t + e of a Q6_K superblock.
+__device__ __forceinline__ void q6k_b(const FragQ6K& f, int g, int st, h8& bh, h8& bl) {
+  const int s = g & 1, t = st >> 1, e = st & 1;
   const uint32_t qa[4] = {f.qa.x, f.qa.y, f.qa.z, f.qa.w};
   const uint32_t qb[4] = {f.qb.x, f.qb.y, f.qb.z, f.qb.w};
   const uint32_t qh[4] = {f.qh.x, f.qh.y, f.qh.z, f.qh.w};
-#pragma unroll
-  for (int t = 0; t < 4; t++) {
-    // scale byte index s + 2t within the 8 scales of this half
-    const uint32_t word = (t < 2) ? f.sc.x : f.sc.y;
-    const int sc = (int)(int8_t)((word >> (8 * ((s + 2 * t) & 3))) & 0xFF);
-    const int shv = sc >> 4, slv = sc & 15;
-    h2 sh_s, sh_c, sl_s, sl_c;
-    if (t < 2) {  // value = 1024 + q6
-      sh_s = hsplat((float)shv); sh_c = hsplat(-1056.0f * (float)shv);
-      sl_s = hsplat((float)slv); sl_c = hsplat(-1056.0f * (float)slv);
-    } else {      // value = 1024 + 16*q6
-      sh_s = hsplat((float)shv * 0.0625f); sh_c = hsplat(-96.0f * (float)shv);
-      sl_s = hsplat((float)slv * 0.0625f); sl_c = hsplat(-96.0f * (float)slv);
-    }
-    const uint32_t* ql = (t & 1) ? qb : qa;
-#pragma unroll
-    for (int e = 0; e < 2; e++) {
-      uint32_t uh[4], ul[4];
-#pragma unroll
-      for (int i = 0; i < 2; i++) {
-        const uint32_t wq = ql[2 * e + i], hq = qh[2 * e + i];
-        uint32_t v1, v2;
-        if (t < 2) {
-          // qh bits 2t,2t+1 -> bits 4,5 of each byte, under the low nibble
-          const uint32_t z = bfi(0x30303030u, hq << (4 - 2 * t), wq);
-          v1 = perm(C64, z, SEL_B0_E_B1_E) & 0x643F643Fu;
-          v2 = perm(C64, z, SEL_B2_E_B3_E) & 0x643F643Fu;
-        } else {
-          // high nibble at bits 4-7, qh bits 2t,2t+1 at bits 8,9 under 0x64
-          const uint32_t hx = ((hq >> (2 * t)) & 0x03030303u) | C64;
-          v1 = perm(hx, wq, SEL_X_B01) & 0x67F067F0u;
-          v2 = perm(hx, wq, SEL_X_B23) & 0x67F067F0u;
-        }
-        uh[2 * i] = pk_fma(v1, sh_s, sh_c);
-        uh[2 * i + 1] = pk_fma(v2, sh_s, sh_c);
-        ul[2 * i] = pk_fma(v1, sl_s, sl_c);
-        ul[2 * i + 1] = pk_fma(v2, sl_s, sl_c);
-      }
-      o.bh[2 * t + e] = mk_h8(uh[0], uh[1], uh[2], uh[3]);
-      o.bl[2 * t + e] = mk_h8(ul[0], ul[1], ul[2], ul[3]);
-    }
+  // scale byte index s + 2t within the 8 scales of this half
+  const uint32_t word = (t < 2) ? f.sc.x : f.sc.y;
+  const int sc = (int)(int8_t)((word >> (8 * ((s + 2 * t) & 3))) & 0xFF);
+  const int shv = sc >> 4, slv = sc & 15;
+  h2 sh_s, sh_c, sl_s, sl_c;
+  if (t < 2) {  // value = 1024 + q6
+    sh_s = hsplat((float)shv); sh_c = hsplat(-1056.0f * (float)shv);
+    sl_s = hsplat((float)slv); sl_c = hsplat(-1056.0f * (float)slv);
+  } else {      // value = 1024 + 16*q6
+    sh_s = hsplat((float)shv * 0.0625f); sh_c = hsplat(-96.0f * (float)shv);
+    sl_s = hsplat((float)slv * 0.0625f); sl_c = hsplat(-96.0f * (float)slv);
   }
+  const uint32_t* ql = (t & 1) ? qb : qa;
+  uint32_t uh[4], ul[4];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const uint32_t wq = ql[2 * e + i], hq = qh[2 * e + i];
+    uint32_t v1, v2;
+    if (t < 2) {
+      // qh bits 2t,2t+1 -> bits 4,5 of each byte, under the low nibble
+      const uint32_t z = bfi(0x30303030u, hq << (4 - 2 * t), wq);
+      v1 = perm(C64, z, SEL_B0_E_B1_E) & 0x643F643Fu;
+      v2 = perm(C64, z, SEL_B2_E_B3_E) & 0x643F643Fu;
+    } else {
+      // high nibble at bits 4-7, qh bits 2t,2t+1 at bits 8,9 under 0x64
+      const uint32_t hx = ((hq >> (2 * t)) & 0x03030303u) | C64;
+      v1 = perm(hx, wq, SEL_X_B01) & 0x67F067F0u;
+      v2 = perm(hx, wq, SEL_X_B23) & 0x67F067F0u;
+    }
+    uh[2 * i] = pk_fma(v1, sh_s, sh_c);
+    uh[2 * i + 1] = pk_fma(v2, sh_s, sh_c);
+    ul[2 * i] = pk_fma(v1, sl_s, sl_c);
+    ul[2 * i + 1] = pk_fma(v2, sl_s, sl_c);
+  }
+  bh = mk_h8(uh[0], uh[1], uh[2], uh[3]);
+  bl = mk_h8(ul[0], ul[1], ul[2], ul[3]);
+}
+__device__ __forceinline__ void decode_q6k(const FragQ6K& f, int g, DecQ6& o) {
+#pragma unroll
+  for (int st = 0; st < 8; st++) q6k_b(f, g, st, o.bh[st], o.bl[st]);
   o.d = f16_bits_to_f32(f.d);
 }
 

@@ -115,6 +115,14 @@ struct GemmArgs {
   int M, N, K;
   int units;
 };
+struct LtArgs {
+  const void* w;
+  const void* x;
+  const void* xs;
+  void* y;
+  long long row_bytes;
+  int M, N, K, units;
+};
 struct DequantArgs {
   const void* w;
   float* out;
@@ -131,6 +139,9 @@ struct DeviceModule {
   hipFunction_t gemv[6][2][2] = {};  // [format][x f32][y f16]
   hipFunction_t dequant[6] = {};
   hipFunction_t gemm[6][2][2] = {};  // K-quant formats only
+  hipFunction_t gemm2[6][2][2][2] = {};  // [format][NT-1][MT/8-1][y f16], fp16 x
+  hipFunction_t xsums = nullptr;
+  int cus = 0;                        // compute units of the device
 };
 DeviceModule g_dev[kMaxDevices];
 
@@ -144,6 +155,7 @@ void load_module(DeviceModule& d, int dev) {
     d.err = std::string("device is ") + prop.gcnArchName + ", this library is built for gfx950 only";
     return;
   }
+  d.cus = prop.multiProcessorCount;
   hipError_t e = hipModuleLoadData(&d.mod, cq_hsaco_image);
   if (e != hipSuccess) {
     d.err = std::string("hipModuleLoadData: ") + hipGetErrorString(e);
@@ -169,12 +181,25 @@ void load_module(DeviceModule& d, int dev) {
             return;
           }
         }
+      for (int nt = 1; nt <= 2; nt++)
+        for (int mt = 8; mt <= 16; mt += 8)
+          for (int yt = 0; yt < 2; yt++) {
+            snprintf(name, sizeof name, "cq_gemm2_%s_n%d_m%d_y%s", fn, nt, mt, yt ? "f16" : "f32");
+            if (hipModuleGetFunction(&d.gemm2[fi][nt - 1][mt / 8 - 1][yt], d.mod, name) != hipSuccess) {
+              d.err = std::string("missing kernel ") + name;
+              return;
+            }
+          }
     }
     snprintf(name, sizeof name, "cq_dequant_%s", fn);
     if (hipModuleGetFunction(&d.dequant[fi], d.mod, name) != hipSuccess) {
       d.err = std::string("missing kernel ") + name;
       return;
     }
+  }
+  if (hipModuleGetFunction(&d.xsums, d.mod, "cq_xsums_f16") != hipSuccess) {
+    d.err = "missing kernel cq_xsums_f16";
+    return;
   }
   d.status = CQ_OK;
 }
@@ -340,6 +365,54 @@ static cq_status launch_gemv(DeviceModule* dm, const cq_weight* w, const void* x
   return CQ_OK;
 }
 
+// Large-tile prefill GEMM (cq_gemm2_*, fp16 x, K-quants): 4 waves x NT
+// 16-row weight tiles x 16*MT activation rows per workgroup; for Q4_K/Q5_K a
+// cq_xsums_f16 pass first writes the activation sub-block sums its min term
+// uses.  MT = 16 once m exceeds one 128-row block; NT = 2 when that still
+// gives every compute unit a workgroup.  COMBS_GEMM2_NT / COMBS_GEMM2_MT force them.
+static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* x, int64_t m, void* y, int yt,
+                              hipStream_t s) {
+  const int fi = fmt_index(w->format);
+  LtArgs a;
+  a.w = w->dev;
+  a.x = x;
+  a.xs = nullptr;
+  a.y = y;
+  a.row_bytes = (long long)(w->nbytes / (size_t)w->n);
+  a.M = (int)m;
+  a.N = (int)w->n;
+  a.K = (int)w->k;
+  a.units = (int)(w->k / 256);
+  int mt = env_int("COMBS_GEMM2_MT", 0);
+  if (mt != 8 && mt != 16) mt = m > 128 ? 16 : 8;
+  const long long mblk = (m + 16 * mt - 1) / (16 * mt);
+  int nt = env_int("COMBS_GEMM2_NT", 0);
+  if (nt != 1 && nt != 2) nt = (w->n + 127) / 128 * mblk >= dm->cus ? 2 : 1;
+  const long long gx = (w->n + 64 * nt - 1) / (64 * nt);
+  if (gx > 0x7fffffffLL || mblk > 65535) return fail(CQ_ERR_BAD_SHAPE, "grid too large");
+  void* ws = nullptr;
+  if (w->format != CQ_Q6_K) {
+    // Stream-ordered scratch for the sums: no state shared between streams,
+    // and recorded as allocation nodes when the stream is being captured.
+    const long long sums = m * a.units * 8;  // one thread per (row, superblock, sub-block)
+    HIP_TRY(hipMallocAsync(&ws, (size_t)sums * 4, s));
+    a.xs = ws;
+    int M = a.M, K = a.K;
+    void* sp[] = {(void*)&x, &ws, &M, &K};
+    hipError_t e = hipModuleLaunchKernel(dm->xsums, (unsigned)((sums + 255) / 256), 1, 1, 256, 1, 1, 0, s, sp, nullptr);
+    if (e != hipSuccess) {
+      (void)hipFreeAsync(ws, s);
+      return fail(CQ_ERR_HIP, "cq_xsums_f16 launch: %s", hipGetErrorString(e));
+    }
+  }
+  void* params[] = {&a};
+  hipError_t e = hipModuleLaunchKernel(dm->gemm2[fi][nt - 1][mt / 8 - 1][yt], (unsigned)gx, (unsigned)mblk, 1, 256, 1,
+                                       1, 0, s, params, nullptr);
+  if (ws) HIP_TRY(hipFreeAsync(ws, s));
+  if (e != hipSuccess) return fail(CQ_ERR_HIP, "cq_gemm2 launch: %s", hipGetErrorString(e));
+  return CQ_OK;
+}
+
 // Prefill GEMM (cq_gemm_*, K-quants): workgroups of nw waves x 16 weight rows
 // and 64 (fp16 x) or 32 (fp32 x) activation rows.
 static cq_status launch_gemm(DeviceModule* dm, const cq_weight* w, const void* x, int xt, int64_t m, void* y, int yt,
@@ -354,6 +427,7 @@ static cq_status launch_gemm(DeviceModule* dm, const cq_weight* w, const void* x
   a.N = (int)w->n;
   a.K = (int)w->k;
   a.units = (int)(w->k / 256);
+  if (!xt && env_int("COMBS_GEMM_KERNEL", 2) == 2) return launch_gemm2(dm, w, x, m, y, yt, s);
   int nw = env_int("COMBS_GEMM_WAVES", 4);
   if (nw < 4 || nw > 8) nw = 4;  // the activation staging assumes >= 256 threads
   const int mb = xt ? 32 : 64;

@@ -4,9 +4,12 @@
 // up with hipModuleGetFunction:
 //   cq_gemv_<fmt>_x<f16|f32>_y<f32|f16>   decode GEMV (m-tiles of 16)
 //   cq_gemm_<fmt>_x<f16|f32>_y<f32|f16>   prefill dequant-GEMM (K-quants)
+//   cq_gemm2_<fmt>_n<1|2>_m<8|16>_y<f32|f16>  prefill dequant-GEMM, large tiles, fp16 x
+//   cq_xsums_f16                          activation sub-block sums for its min term
 //   cq_dequant_<fmt>                      bit-exact dequantisation
 #include "cq_gemv.h"
 #include "cq_gemm.h"
+#include "cq_gemm2.h"
 #include "cq_dequant.h"
 
 #define GEMV_KERNEL(NAME, FMT, XT, YT)                                               \
@@ -53,3 +56,35 @@ DEQUANT_KERNEL(q6_k, CQ_Q6_K)
 GEMM_FMT(q4_k, CQ_Q4_K)
 GEMM_FMT(q5_k, CQ_Q5_K)
 GEMM_FMT(q6_k, CQ_Q6_K)
+
+#define GEMM2_KERNEL(NAME, FMT, YT, NT, MT)                                           \
+  extern "C" __global__ void __launch_bounds__(256) NAME(const LtArgs a) {             \
+    gemm2_body<FMT, YT, NT, MT>(a);                                                    \
+  }
+GEMM2_KERNEL(cq_gemm2_q4_k_n1_m8_yf32, CQ_Q4_K, 0, 1, 8)
+GEMM2_KERNEL(cq_gemm2_q4_k_n1_m8_yf16, CQ_Q4_K, 1, 1, 8)
+GEMM2_KERNEL(cq_gemm2_q4_k_n1_m16_yf32, CQ_Q4_K, 0, 1, 16)
+GEMM2_KERNEL(cq_gemm2_q4_k_n1_m16_yf16, CQ_Q4_K, 1, 1, 16)
+GEMM2_KERNEL(cq_gemm2_q4_k_n2_m8_yf32, CQ_Q4_K, 0, 2, 8)
+GEMM2_KERNEL(cq_gemm2_q4_k_n2_m8_yf16, CQ_Q4_K, 1, 2, 8)
+GEMM2_KERNEL(cq_gemm2_q4_k_n2_m16_yf32, CQ_Q4_K, 0, 2, 16)
+GEMM2_KERNEL(cq_gemm2_q4_k_n2_m16_yf16, CQ_Q4_K, 1, 2, 16)
+GEMM2_KERNEL(cq_gemm2_q5_k_n1_m8_yf32, CQ_Q5_K, 0, 1, 8)
+GEMM2_KERNEL(cq_gemm2_q5_k_n1_m8_yf16, CQ_Q5_K, 1, 1, 8)
+GEMM2_KERNEL(cq_gemm2_q5_k_n1_m16_yf32, CQ_Q5_K, 0, 1, 16)
+GEMM2_KERNEL(cq_gemm2_q5_k_n1_m16_yf16, CQ_Q5_K, 1, 1, 16)
+GEMM2_KERNEL(cq_gemm2_q5_k_n2_m8_yf32, CQ_Q5_K, 0, 2, 8)
+GEMM2_KERNEL(cq_gemm2_q5_k_n2_m8_yf16, CQ_Q5_K, 1, 2, 8)
+GEMM2_KERNEL(cq_gemm2_q5_k_n2_m16_yf32, CQ_Q5_K, 0, 2, 16)
+GEMM2_KERNEL(cq_gemm2_q5_k_n2_m16_yf16, CQ_Q5_K, 1, 2, 16)
+GEMM2_KERNEL(cq_gemm2_q6_k_n1_m8_yf32, CQ_Q6_K, 0, 1, 8)
+GEMM2_KERNEL(cq_gemm2_q6_k_n1_m8_yf16, CQ_Q6_K, 1, 1, 8)
+GEMM2_KERNEL(cq_gemm2_q6_k_n1_m16_yf32, CQ_Q6_K, 0, 1, 16)
+GEMM2_KERNEL(cq_gemm2_q6_k_n1_m16_yf16, CQ_Q6_K, 1, 1, 16)
+GEMM2_KERNEL(cq_gemm2_q6_k_n2_m8_yf32, CQ_Q6_K, 0, 2, 8)
+GEMM2_KERNEL(cq_gemm2_q6_k_n2_m8_yf16, CQ_Q6_K, 1, 2, 8)
+GEMM2_KERNEL(cq_gemm2_q6_k_n2_m16_yf32, CQ_Q6_K, 0, 2, 16)
+GEMM2_KERNEL(cq_gemm2_q6_k_n2_m16_yf16, CQ_Q6_K, 1, 2, 16)
+extern "C" __global__ void __launch_bounds__(256) cq_xsums_f16(const _Float16* x, _Float16* xs, int M, int K) {
+  xsums_body(x, xs, M, K);
+}

@@ -160,20 +160,58 @@ KQ = [QuantFormat.Q4K, QuantFormat.Q5K, QuantFormat.Q6K]
 
 
 @pytest.mark.parametrize("fmt", KQ)
-@pytest.mark.parametrize("m", [1, 17, 64, 100, 130])
-def test_gemm_parity(cuda, fmt, m):
+@pytest.mark.parametrize("m", [1, 17, 64, 100, 130, 300])
+@pytest.mark.parametrize("kernel", ["1", "2:1:8", "2:2:8", "2:1:16", "2:2:16"])
+def test_gemm_parity(cuda, monkeypatch, fmt, m, kernel):
     """Prefill dequant-GEMM (forced for small m too) vs the oracle, fp16/fp32
-    activations, fp32/fp16 outputs, ragged m and n."""
+    activations, fp32/fp16 outputs, ragged m and n; every kernel and tile
+    shape (kernel:NT:MT)."""
     import torch
+    kern, nt, mt = (kernel.split(":") + ["0", "0"])[:3]
+    monkeypatch.setenv("COMBS_GEMM_KERNEL", kern)
+    monkeypatch.setenv("COMBS_GEMM2_NT", nt)
+    monkeypatch.setenv("COMBS_GEMM2_MT", mt)
     n, k = 300, 1024
     data = synth(fmt, n, k)
     wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
     w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
     x = O.x_pattern(m, k, 11, 29, 14.0, 16.0).reshape(m, k)
     expect = O.ref_matmul(x, wd)
-    print(f"gemm {fmt.name} m={m}", flush=True)
+    print(f"gemm kernel={kernel} {fmt.name} m={m}", flush=True)
     O.assert_close(_run(w, x, torch.float16, torch.float32, path=L.CQ_PATH_GEMM), expect, 1e-3, "x16 y32")
     O.assert_close(_run(w, x, torch.float32, torch.float16, path=L.CQ_PATH_GEMM), expect, 1e-3, "x32 y16")
+
+
+SCALE_OFF = {QuantFormat.Q4K: (0, 144), QuantFormat.Q5K: (0, 176), QuantFormat.Q6K: (208, 210)}
+
+
+@pytest.mark.parametrize("fmt", KQ)
+@pytest.mark.parametrize("nt", ["1", "2"])
+@pytest.mark.parametrize("mt", ["8", "16"])
+def test_gemm_scale_edge_cases(cuda, monkeypatch, fmt, nt, mt):
+    """Superblocks whose d is zero (min term only), subnormal, or 2^12 times
+    larger than their neighbours: the large-tile kernel carries its
+    accumulator in units of the running d and must still match the oracle."""
+    import torch
+    monkeypatch.setenv("COMBS_GEMM2_NT", nt)
+    monkeypatch.setenv("COMBS_GEMM2_MT", mt)
+    off, bb = SCALE_OFF[fmt]
+    n, k, m = 200, 2048, 150
+    data = np.frombuffer(synth(fmt, n, k), dtype=np.uint8).copy()
+    blocks = data.reshape(-1, bb)
+    d = blocks[:, off:off + 2].copy().view(np.float16).reshape(-1)
+    rng = np.random.default_rng(5)
+    pick = rng.integers(0, 6, d.size)
+    d[pick == 0] = 0.0
+    d[pick == 1] = np.float16(3e-7)                      # subnormal
+    d[pick == 2] = (d[pick == 2].astype(np.float32) * 4096).clip(-6e4, 6e4).astype(np.float16)
+    blocks[:, off:off + 2] = d.view(np.uint8).reshape(-1, 2)
+    data = data.tobytes()
+    wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
+    w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
+    x = O.x_pattern(m, k, 7, 23, 12.0, 16.0).reshape(m, k)
+    print(f"scale edges {fmt.name} nt={nt} mt={mt}", flush=True)
+    O.assert_close(_run(w, x, torch.float16, torch.float32, path=L.CQ_PATH_GEMM), O.ref_matmul(x, wd), 1e-3, "gemm")
 
 
 @pytest.mark.parametrize("fmt", KQ)

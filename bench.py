@@ -15,7 +15,8 @@ measures the kernels back to back rather than Python's launch overhead.
 value = algorithmic bytes (GGUF-native weight bytes + x + y) of K steps
         / device time of the K steps (HIP events around the graph replay).
 
-Also reported: the roofline of the dominant kernel (cq_gemv_q4_k_xf16_yf32)
+Also reported: the roofline of the dominant kernel (cq_gemv1_q4_k_yf32, the
+single-row decode GEMV)
 from graphs of single-shape launches, prefill dequant-GEMM TFLOP/s (config 4),
 lm_head Q6_K and batch 4/16, and the reference CPU path (dequantise once,
 dense f32 GEMV per call) timed on this host as cpu_baseline.
@@ -30,6 +31,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+HEADLINE_KERNEL = "cq_gemv1_q4_k_yf32"  # what cq_matmul launches for m = 1, fp16 x, Q4_K
 FP16_PEAK_TFLOPS = 2500.0
 
 
@@ -210,7 +212,7 @@ def main():
 
     # Dominant kernel: launches of one shape back to back in a graph.
     launch, tot_b, tot_us = {}, 0.0, 0.0
-    traffic = load_traffic().get("cq_gemv_q4_k_xf16_yf32", {})
+    traffic = load_traffic().get(HEADLINE_KERNEL, {})
     for s, (n, k) in enumerate(shapes):
         us, _ = graph_time_us(lambda i, s=s: pools[s][i % P].matmul_into(xs[s], ys[s]), 4 * P)
         b = algo_bytes(sizes[s], 1, k, n)
@@ -235,7 +237,7 @@ def main():
                                f"y f32; weight pool {P} x {len(shapes)} buffers ({P * sum(sizes) / 2**30:.2f} GiB)",
                    "global_batch": 1, "parallelism": "none (1 GPU)"},
         "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
-        "roofline": {"bound": "hbm", "kernel": "cq_gemv_q4_k_xf16_yf32", "achieved": round(achieved, 1),
+        "roofline": {"bound": "hbm", "kernel": HEADLINE_KERNEL, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_val,
                      "algorithmic_bytes_per_launch": round(tot_b / len(shapes)), "launches": launch},

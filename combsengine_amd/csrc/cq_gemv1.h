@@ -1,0 +1,269 @@
+// Decode GEMV for a single activation row (m = 1) over K-quant weights:
+// y[n] = sum_k x[k] * W[n, k], streamed at HBM speed.
+//
+// Why not the MFMA GEMV here: with one activation row an MFMA computes 16
+// rows of which one is used, and its lane = weight-row layout makes every
+// wave gather 16 separate 16-byte streams.  This kernel gives each lane one
+// whole superblock instead:
+//   - a wave task is R = max(1, 64 / units) consecutive rows, i.e. one
+//     contiguous span of at most 64 superblocks; lane l loads superblock l
+//     of the span (row l / units, unit l % units) straight into registers
+//     (144 / 176 bytes as 16-byte loads; across the wave the loads cover the
+//     span contiguously);
+//   - a persistent grid of one 4-wave workgroup per compute unit, each wave
+//     walking ~N/(R * 4 * CUs) tasks with its loads one task ahead: early
+//     tasks complete early and their arithmetic overlaps the rest of the
+//     stream (issuing every task's loads at once makes all of them arrive
+//     late and serialises memory and compute);
+//   - the inner products are integer: each 32-value activation block is
+//     staged as three int8 parts, x = s * (h + l/254 + e/254^2) with
+//     s = max|x|/127 (about 22 bits relative to the block maximum, error
+//     <= max|x| * 3.9e-8; two parts, 15 bits, fail the 1e-3 bar on outputs
+//     that cancel), and each lane masks its nibbles in place (q = 0..15 /
+//     0..31 per byte) and accumulates v_dot4_i32_i8 against h, l and e,
+//     exactly in int32; per sub-block the three sums become one fp32 value
+//     scaled by d * sc * s, and the min term uses the fp32 sums of the fp16
+//     activations;
+//   - the lanes of a row are summed with cross-lane adds.
+// The activation row is staged once per workgroup in LDS, padded by 16 bytes
+// every 256 values so that lanes reading different units hit different banks.
+// Four int8 multiply-adds per instruction (against two per fp16 dot) roughly
+// halve the VALU work per weight, which is what lets the weight stream run
+// at memory speed.
+// Replaces qmatmul.rs:881-930 (Q4_K) and :1064-1117 (Q5_K) for m = 1.
+#pragma once
+#include "cq_gemv.h"
+
+#define GV1_WAVES 4
+#define GV1_XMAX 16384                       // largest K staged
+#define GV1_XSTRIDE 272                      // bytes per staged 256-value unit (16 pad)
+
+struct Gv1Args {
+  const uint8_t* w;
+  const _Float16* x;
+  void* y;
+  long long row_bytes;  // units * block bytes
+  int N, K, units;
+  int rows;             // rows per wave task (R)
+  int tasks;            // ceil(N / R)
+};
+
+__shared__ __attribute__((aligned(16))) int8_t gv_xh[GV1_XMAX / 256 * GV1_XSTRIDE];
+__shared__ __attribute__((aligned(16))) int8_t gv_xl[GV1_XMAX / 256 * GV1_XSTRIDE];
+__shared__ __attribute__((aligned(16))) int8_t gv_xe[GV1_XMAX / 256 * GV1_XSTRIDE];
+__shared__ float gv_xs[GV1_XMAX / 32];  // s of each 32-value block
+__shared__ float gv_s[GV1_XMAX / 32];   // sum of each 32-value block (fp32 of the fp16 values)
+
+// The 8 scales and mins of a K-quant superblock header as floats.
+__device__ __forceinline__ void gv1_scales(const u4v& hd, float sc[8], float mn[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    uint32_t s, m;
+    scale_min_k4(j, hd.y, hd.z, hd.w, s, m);
+    sc[j] = (float)s;
+    mn[j] = (float)m;
+  }
+}
+
+// One superblock in registers, as 16-byte chunks.
+template <int FMT>
+struct Gv1Block {
+  static constexpr int NC = FmtTraits<FMT>::bytes / 16;
+  u4v c[NC];
+  __device__ __forceinline__ void load(const uint8_t* p) {
+#pragma unroll
+    for (int i = 0; i < NC; i++) c[i] = ld_u128(p + 16 * i);
+  }
+};
+
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// Partial dot product of one superblock with the staged activations of its
+// unit (xh, xl, xe: 256 int8 each; xs, su: 8 block scales / sums).
+template <int FMT>
+__device__ __forceinline__ float gv1_superblock(const Gv1Block<FMT>& b, const int8_t* xh, const int8_t* xl,
+                                                const int8_t* xe, const float* xs, const float* su) {
+  const u4v hd = b.c[0];
+  float sc[8], mn[8];
+  gv1_scales(hd, sc, mn);
+  const float d = f16_bits_to_f32(hd.x), dmin = f16_bits_to_f32(hd.x >> 16);
+  constexpr int QC = FMT == CQ_Q5_K ? 3 : 1;  // first qs chunk
+  float acc = 0.0f, macc = 0.0f;
+#pragma unroll
+  for (int p = 0; p < 4; p++) {  // sub-block pair: 2p (low nibbles), 2p+1 (high)
+    int ih0 = 0, il0 = 0, ie0 = 0, ih1 = 0, il1 = 0, ie1 = 0;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {  // bytes [16h, 16h+16) of the pair: values 16h .. 16h+15
+      const u4v q = b.c[QC + 2 * p + h];
+      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+      const int o0 = 64 * p + 16 * h, o1 = o0 + 32;
+      const u4v h0 = *(const u4v*)(xh + o0), l0 = *(const u4v*)(xl + o0);
+      const u4v h1 = *(const u4v*)(xh + o1), l1 = *(const u4v*)(xl + o1);
+      const u4v e0 = *(const u4v*)(xe + o0), e1 = *(const u4v*)(xe + o1);
+      const uint32_t xh0[4] = {h0.x, h0.y, h0.z, h0.w}, xl0[4] = {l0.x, l0.y, l0.z, l0.w};
+      const uint32_t xh1[4] = {h1.x, h1.y, h1.z, h1.w}, xl1[4] = {l1.x, l1.y, l1.z, l1.w};
+      const uint32_t xe0[4] = {e0.x, e0.y, e0.z, e0.w}, xe1[4] = {e1.x, e1.y, e1.z, e1.w};
+      uint32_t hb[4] = {0, 0, 0, 0};
+      if constexpr (FMT == CQ_Q5_K) {
+        const u4v qh = b.c[1 + h];
+        hb[0] = qh.x; hb[1] = qh.y; hb[2] = qh.z; hb[3] = qh.w;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+        if constexpr (FMT == CQ_Q5_K) {
+          // 5th bits: qh bit 2p (low values), 2p+1 (high values) -> bit 4 of each byte
+          lo |= ((hb[i] >> (2 * p)) & 0x01010101u) << 4;
+          hi |= ((hb[i] >> (2 * p + 1)) & 0x01010101u) << 4;
+        }
+        ih0 = dot4(lo, xh0[i], ih0);
+        il0 = dot4(lo, xl0[i], il0);
+        ie0 = dot4(lo, xe0[i], ie0);
+        ih1 = dot4(hi, xh1[i], ih1);
+        il1 = dot4(hi, xl1[i], il1);
+        ie1 = dot4(hi, xe1[i], ie1);
+      }
+    }
+    // |il| * 254 + |ie| stays far inside int32: combine exactly, then one conversion
+    const float f0 = __builtin_fmaf((float)(254 * il0 + ie0), 1.0f / 64516.0f, (float)ih0);
+    const float f1 = __builtin_fmaf((float)(254 * il1 + ie1), 1.0f / 64516.0f, (float)ih1);
+    acc = __builtin_fmaf(sc[2 * p] * xs[2 * p], f0, acc);
+    acc = __builtin_fmaf(sc[2 * p + 1] * xs[2 * p + 1], f1, acc);
+    macc = __builtin_fmaf(mn[2 * p], su[2 * p], macc);
+    macc = __builtin_fmaf(mn[2 * p + 1], su[2 * p + 1], macc);
+  }
+  return d * acc - dmin * macc;
+}
+
+template <int FMT, int YT>
+__device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
+  constexpr int BB = FmtTraits<FMT>::bytes;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lanes_used = a.rows * a.units;
+  const int myrow = lane / a.units, myunit = lane - myrow * a.units;
+  const int stride = gridDim.x * GV1_WAVES;
+  // lane's superblock of task t (lanes past the task's rows reread its first)
+  auto block_ptr = [&](int t) {
+    const int r0 = t * a.rows;
+    const int nsb = min(a.rows, a.N - r0) * a.units;
+    return a.w + ((size_t)r0 * a.units + (lane < nsb ? lane : 0)) * BB;
+  };
+  // Load order matters (the vector-memory counter retires in order): the
+  // activation chunks first, then the first task's weights, so that staging
+  // x into LDS waits only for x while the weights' HBM latency runs on.
+  constexpr int XL = GV1_XMAX / 8 / (64 * GV1_WAVES);  // 16-byte x chunks per thread, at most
+  u4v xv[XL];
+  // (Branch-free: indices past the end are clamped, so chunks may be loaded
+  // and stored twice with the same value; control-flow joins would make the
+  // compiler wait for every outstanding load.)
+  const int xc_last = a.K / 8 - 1;
+#pragma unroll
+  for (int i = 0; i < XL; i++) {
+    const int c = min((int)threadIdx.x + 64 * GV1_WAVES * i, xc_last);
+    xv[i] = ld_u128((const uint8_t*)(a.x + 8 * c));
+  }
+  int t = blockIdx.x * GV1_WAVES + wave;
+  Gv1Block<FMT> cur, nxt;
+  cur.load(block_ptr(min(t, a.tasks - 1)));
+  __builtin_amdgcn_sched_barrier(0);  // keep the weight loads ahead of the staging
+  // Quantise: thread c holds chunk c (8 values); the 4 threads of a 32-value
+  // block share its max and sum.  Threads past the end hold a copy of the
+  // last chunk and store nothing.
+#pragma unroll
+  for (int i = 0; i < XL; i++) {
+    if (64 * GV1_WAVES * i > xc_last) break;  // uniform
+    const int craw = (int)threadIdx.x + 64 * GV1_WAVES * i;
+    const int c = min(craw, xc_last);
+    const uint32_t wv[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+    float v[8], mx = 0.0f, sm = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      v[2 * e] = (float)as_h2(wv[e])[0];
+      v[2 * e + 1] = (float)as_h2(wv[e])[1];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      mx = fmaxf(mx, fabsf(v[e]));
+      sm += v[e];
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+    sm += __shfl_xor(sm, 1, 64);
+    sm += __shfl_xor(sm, 2, 64);
+    const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
+    uint32_t hw[2] = {0, 0}, lw[2] = {0, 0}, ew[2] = {0, 0};
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      // y = x/s in [-127, 127]; residuals after each rounding are in [-0.5, 0.5]
+      const float y = v[e] * inv;
+      const float hv = __builtin_rintf(y);
+      const float r1 = (y - hv) * 254.0f;
+      const float lv = __builtin_rintf(r1);
+      const float ev = __builtin_rintf((r1 - lv) * 254.0f);
+      const int sh = 8 * (e & 3);
+      hw[e >> 2] |= (uint32_t)((int)hv & 0xFF) << sh;
+      lw[e >> 2] |= (uint32_t)((int)lv & 0xFF) << sh;
+      ew[e >> 2] |= (uint32_t)((int)ev & 0xFF) << sh;
+    }
+    if (craw <= xc_last) {
+      const int off = (c >> 5) * GV1_XSTRIDE + 8 * (c & 31);
+      *(u2v*)(gv_xh + off) = u2v{hw[0], hw[1]};
+      *(u2v*)(gv_xl + off) = u2v{lw[0], lw[1]};
+      *(u2v*)(gv_xe + off) = u2v{ew[0], ew[1]};
+      if ((c & 3) == 0) {
+        gv_xs[c >> 2] = mx * (1.0f / 127.0f);
+        gv_s[c >> 2] = sm;
+      }
+    }
+  }
+  __syncthreads();
+
+  auto task_compute = [&](const Gv1Block<FMT>& blk, int tt) {
+    const int r0 = tt * a.rows;
+    const int nrows = min(a.rows, a.N - r0);
+    float part = 0.0f;
+    if (lane < lanes_used && myrow < nrows)
+      part = gv1_superblock<FMT>(blk, gv_xh + myunit * GV1_XSTRIDE, gv_xl + myunit * GV1_XSTRIDE,
+                                 gv_xe + myunit * GV1_XSTRIDE, gv_xs + 8 * myunit, gv_s + 8 * myunit);
+    if ((a.units & (a.units - 1)) == 0) {
+      // a row's lanes form an aligned group of `units` lanes: butterfly within it
+      for (int o = a.units >> 1; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+      if (myunit == 0 && myrow < nrows) {
+        if (YT) ((_Float16*)a.y)[r0 + myrow] = (_Float16)part;
+        else ((float*)a.y)[r0 + myrow] = part;
+      }
+    } else {
+      for (int q = 0; q < a.rows; q++) {
+        float v = myrow == q ? part : 0.0f;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+        if (lane == 0 && q < nrows) {
+          if (YT) ((_Float16*)a.y)[r0 + q] = (_Float16)v;
+          else ((float*)a.y)[r0 + q] = v;
+        }
+      }
+    }
+  };
+  // This wave's tasks t, t + stride, ...: n of them.  Loads run one task
+  // ahead of the compute, each compute call sits on a path of its own so
+  // that the compiler's in-order load counters wait exactly for the task
+  // it needs.
+  const int n = t < a.tasks ? (a.tasks - 1 - t) / stride + 1 : 0;
+  for (int j = 0; j < n; j += 2, t += 2 * stride) {
+    if (j + 1 < n) {
+      nxt.load(block_ptr(t + stride));
+      task_compute(cur, t);
+      if (j + 2 < n) {
+        cur.load(block_ptr(t + 2 * stride));
+        task_compute(nxt, t + stride);
+      } else {
+        task_compute(nxt, t + stride);
+      }
+    } else {
+      task_compute(cur, t);
+    }
+  }
+}

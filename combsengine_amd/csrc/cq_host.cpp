@@ -123,6 +123,13 @@ struct LtArgs {
   long long row_bytes;
   int M, N, K, units;
 };
+struct Gv1Args {
+  const void* w;
+  const void* x;
+  void* y;
+  long long row_bytes;
+  int N, K, units, rows, tasks;
+};
 struct DequantArgs {
   const void* w;
   float* out;
@@ -141,6 +148,7 @@ struct DeviceModule {
   hipFunction_t gemm[6][2][2] = {};  // K-quant formats only
   hipFunction_t gemm2[6][2][2][2] = {};  // [format][NT-1][MT/8-1][y f16], fp16 x
   hipFunction_t xsums = nullptr;
+  hipFunction_t gemv1[6][2] = {};     // [format][y f16]: Q4_K, Q5_K only
   int cus = 0;                        // compute units of the device
 };
 DeviceModule g_dev[kMaxDevices];
@@ -195,6 +203,16 @@ void load_module(DeviceModule& d, int dev) {
     if (hipModuleGetFunction(&d.dequant[fi], d.mod, name) != hipSuccess) {
       d.err = std::string("missing kernel ") + name;
       return;
+    }
+  }
+  for (int fi = 0; fi < 6; fi++) {
+    if (kFormats[fi] != CQ_Q4_K && kFormats[fi] != CQ_Q5_K) continue;
+    for (int yt = 0; yt < 2; yt++) {
+      snprintf(name, sizeof name, "cq_gemv1_%s_y%s", fmt_name(kFormats[fi]), yt ? "f16" : "f32");
+      if (hipModuleGetFunction(&d.gemv1[fi][yt], d.mod, name) != hipSuccess) {
+        d.err = std::string("missing kernel ") + name;
+        return;
+      }
     }
   }
   if (hipModuleGetFunction(&d.xsums, d.mod, "cq_xsums_f16") != hipSuccess) {
@@ -365,6 +383,34 @@ static cq_status launch_gemv(DeviceModule* dm, const cq_weight* w, const void* x
   return CQ_OK;
 }
 
+// Decode GEMV for one fp16 activation row (cq_gemv1_*, Q4_K/Q5_K): wave
+// tasks of max(1, 64/units) whole rows, a persistent grid of one 4-wave
+// workgroup per compute unit.  Returns false when the shape is not covered.
+constexpr int kGv1Waves = 4, kGv1MaxK = 16384;
+static bool gemv1_fits(const cq_weight* w) {
+  return (w->format == CQ_Q4_K || w->format == CQ_Q5_K) && w->k <= kGv1MaxK && w->k / 256 <= 64;
+}
+static cq_status launch_gemv1(DeviceModule* dm, const cq_weight* w, const void* x, void* y, int yt, hipStream_t s) {
+  const int fi = fmt_index(w->format);
+  Gv1Args a;
+  a.w = w->dev;
+  a.x = x;
+  a.y = y;
+  a.row_bytes = (long long)(w->nbytes / (size_t)w->n);
+  a.N = (int)w->n;
+  a.K = (int)w->k;
+  a.units = (int)(w->k / 256);
+  a.rows = a.units >= 64 ? 1 : 64 / a.units;
+  a.tasks = (int)((w->n + a.rows - 1) / a.rows);
+  const int wgs = (a.tasks + kGv1Waves - 1) / kGv1Waves;
+  int cap = env_int("COMBS_GEMV1_GRID", dm->cus);
+  if (cap < 1) cap = 1;
+  const int grid = wgs < cap ? wgs : cap;
+  void* params[] = {&a};
+  HIP_TRY(hipModuleLaunchKernel(dm->gemv1[fi][yt], (unsigned)grid, 1, 1, 64 * kGv1Waves, 1, 1, 0, s, params, nullptr));
+  return CQ_OK;
+}
+
 // Large-tile prefill GEMM (cq_gemm2_*, fp16 x, K-quants): 4 waves x NT
 // 16-row weight tiles x 16*MT activation rows per workgroup; for Q4_K/Q5_K a
 // cq_xsums_f16 pass first writes the activation sub-block sums its min term
@@ -458,6 +504,8 @@ cq_status cq_matmul_path(const cq_weight* w, const void* x, int x_dtype, int64_t
   const bool kq = block_values(w->format) == 256;
   if (kq && (path == CQ_PATH_GEMM || (path == CQ_PATH_AUTO && m > 16)))
     return launch_gemm(dm, w, x, xt, m, y, yt, (hipStream_t)stream);
+  if (m == 1 && !xt && path != CQ_PATH_GEMV && gemv1_fits(w) && env_int("COMBS_GEMV1", 1))
+    return launch_gemv1(dm, w, x, y, yt, (hipStream_t)stream);
   return launch_gemv(dm, w, x, xt, m, y, yt, (hipStream_t)stream);
 }
 

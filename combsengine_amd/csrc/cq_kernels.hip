@@ -3,11 +3,13 @@
 // hipModuleLoadData.  Kernel names are extern "C" so the host can look them
 // up with hipModuleGetFunction:
 //   cq_gemv_<fmt>_x<f16|f32>_y<f32|f16>   decode GEMV (m-tiles of 16)
+//   cq_gemv1_<fmt>_y<f32|f16>             decode GEMV, one fp16 activation row, K-quants
 //   cq_gemm_<fmt>_x<f16|f32>_y<f32|f16>   prefill dequant-GEMM (K-quants)
 //   cq_gemm2_<fmt>_n<1|2>_m<8|16>_y<f32|f16>  prefill dequant-GEMM, large tiles, fp16 x
 //   cq_xsums_f16                          activation sub-block sums for its min term
 //   cq_dequant_<fmt>                      bit-exact dequantisation
 #include "cq_gemv.h"
+#include "cq_gemv1.h"
 #include "cq_gemm.h"
 #include "cq_gemm2.h"
 #include "cq_dequant.h"
@@ -88,3 +90,12 @@ GEMM2_KERNEL(cq_gemm2_q6_k_n2_m16_yf16, CQ_Q6_K, 1, 2, 16)
 extern "C" __global__ void __launch_bounds__(256) cq_xsums_f16(const _Float16* x, _Float16* xs, int M, int K) {
   xsums_body(x, xs, M, K);
 }
+
+#define GEMV1_KERNEL(NAME, FMT, YT)                                                    \
+  extern "C" __global__ void __launch_bounds__(64 * GV1_WAVES) NAME(const Gv1Args a) { \
+    gemv1_body<FMT, YT>(a);                                                            \
+  }
+GEMV1_KERNEL(cq_gemv1_q4_k_yf32, CQ_Q4_K, 0)
+GEMV1_KERNEL(cq_gemv1_q4_k_yf16, CQ_Q4_K, 1)
+GEMV1_KERNEL(cq_gemv1_q5_k_yf32, CQ_Q5_K, 0)
+GEMV1_KERNEL(cq_gemv1_q5_k_yf16, CQ_Q5_K, 1)

@@ -159,6 +159,25 @@ def test_gemv_large_and_ragged(cuda, fmt, n, k, m):
 KQ = [QuantFormat.Q4K, QuantFormat.Q5K, QuantFormat.Q6K]
 
 
+@pytest.mark.parametrize("fmt", [QuantFormat.Q4K, QuantFormat.Q5K])
+@pytest.mark.parametrize("n,k", [(300, 4096), (35, 512), (97, 3584), (50, 5120), (70, 14336), (130, 16384), (1, 256)])
+@pytest.mark.parametrize("gemv1", ["1", "0"])
+def test_gemv_single_row(cuda, monkeypatch, fmt, n, k, gemv1):
+    """m = 1 fp16 decode through the row-streaming kernel (gemv1=1: wave
+    tasks of 64/units whole rows, ragged last task, units from 1 to 64) and
+    through the 16-row MFMA kernel (gemv1=0), fp32 and fp16 outputs."""
+    import torch
+    monkeypatch.setenv("COMBS_GEMV1", gemv1)
+    data = synth(fmt, n, k)
+    wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
+    w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
+    x = O.x_pattern(1, k, 13, 31, 15.0, 16.0).reshape(1, k)
+    expect = O.ref_matmul(x, wd)
+    print(f"gemv1={gemv1} {fmt.name} n={n} k={k}", flush=True)
+    O.assert_close(_run(w, x, torch.float16, torch.float32), expect, 1e-3, "y32")
+    O.assert_close(_run(w, x, torch.float16, torch.float16), expect, 1e-3, "y16")
+
+
 @pytest.mark.parametrize("fmt", KQ)
 @pytest.mark.parametrize("m", [1, 17, 64, 100, 130, 300])
 @pytest.mark.parametrize("kernel", ["1", "2:1:8", "2:2:8", "2:1:16", "2:2:16"])

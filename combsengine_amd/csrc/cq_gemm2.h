@@ -28,6 +28,9 @@
 //     activation sub-block sums (computed once per launch by cq_xsums_f16,
 //     staged in LDS as fp16 hi + lo of sum/64) against the exact 6-bit mins,
 //     folded into acc with one FMA per register.
+//   - When the tile grid cannot cover the compute units (few weight rows,
+//     long K: the o / down projections), K is split over blockIdx.z; each
+//     slice writes fp32 partials and cq_splitk_reduce_* sums them into y.
 //   - Q6_K's i8 scale is split sc = 16*sh + sl; the operands (q-32)*sh and
 //     (q-32)*sl/16 are both exact in fp16 and share the accumulator, whose
 //     units are then 16*d.
@@ -51,8 +54,10 @@ struct LtArgs {
   const _Float16* x;   // [M][K]
   const _Float16* xs;  // [M][K/256][16]: per superblock the 8 sub-block sums/64, fp16 hi then lo
   void* y;             // [M][N] fp32 or fp16
+  float* part;         // split K: [splits][M][N] fp32 partial sums (y unused), else null
   long long row_bytes;
   int M, N, K, units;  // units = K / 256
+  int usplit;          // superblocks per K slice (blockIdx.z); units when not split
 };
 
 // Distinct static arrays: the compiler can then see that reading one buffer
@@ -371,10 +376,13 @@ __device__ __forceinline__ void gemm2_body(const LtArgs& a) {
   lt_tile(bx, by);
   const int n0 = (bx * LT_WAVES + s.wave) * 16 * NT;
   const int m0 = by * 16 * MT;
+  // K slice of this workgroup: superblocks [ub, ub + nu)
+  const int ub = blockIdx.z * a.usplit;
+  const int nu = min(a.usplit, a.units - ub);
 #pragma unroll
   for (int t = 0; t < NT; t++) {
     const int row = min(n0 + 16 * t + s.j, a.N - 1);
-    s.wr[t] = a.w + (size_t)row * a.row_bytes;
+    s.wr[t] = a.w + (size_t)row * a.row_bytes + (size_t)ub * FmtTraits<FMT>::bytes;
     s.deff[t] = 1.0f;
     s.kk[t] = 0.0f;
     s.live[t] = true;
@@ -395,7 +403,7 @@ __device__ __forceinline__ void gemm2_body(const LtArgs& a) {
   const uint32_t dsw = 16 * ((s.lane & 15) ^ lt_sw<FMT>(dr));
   const uint32_t xoff0 = (m0 + dr) * K2 + dsw, xmax = (uint32_t)(a.M - 1) * K2 + dsw;
   auto dma_x = [&](_Float16* buf, int step) {
-    const char* base = (const char*)a.x + step * (LT_KC * 2);
+    const char* base = (const char*)a.x + (2 * ub + step) * (LT_KC * 2);
 #pragma unroll
     for (int ii = 0; ii < MT; ii++) {
       const uint32_t off = min(xoff0 + ii * 16 * K2, xmax);
@@ -411,7 +419,7 @@ __device__ __forceinline__ void gemm2_body(const LtArgs& a) {
       const int i = s.wave + LT_WAVES * ii;
       if (i < MT / 2) {
         const int row = min(m0 + 32 * i + srow, a.M - 1);
-        const _Float16* src = a.xs + ((size_t)row * a.units + u) * 16 + 8 * (s.lane & 1);
+        const _Float16* src = a.xs + ((size_t)row * a.units + ub + u) * 16 + 8 * (s.lane & 1);
         __builtin_amdgcn_global_load_lds((lt_glb_t*)src, (lt_lds_t*)(buf + i * 512), 16, 0, 0);
       }
     }
@@ -423,7 +431,7 @@ __device__ __forceinline__ void gemm2_body(const LtArgs& a) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
-  const int steps = 2 * a.units;
+  const int steps = 2 * nu;
   // One step: prefetch the next (activation DMA, its sums at a superblock
   // boundary, the weight bytes), compute this one, then wait and barrier.
   auto step = [&](auto hc, auto pc, int i) {
@@ -465,7 +473,8 @@ __device__ __forceinline__ void gemm2_body(const LtArgs& a) {
         const int m = m0 + 16 * tm + 4 * s.g + r, n = n0 + 16 * t + s.j;
         if (m < a.M && n < a.N) {
           const float v = s.deff[t] * s.acc[t][tm][r];
-          if (YT) ((_Float16*)a.y)[(size_t)m * a.N + n] = (_Float16)v;
+          if (a.part) a.part[((size_t)blockIdx.z * a.M + m) * a.N + n] = v;
+          else if (YT) ((_Float16*)a.y)[(size_t)m * a.N + n] = (_Float16)v;
           else ((float*)a.y)[(size_t)m * a.N + n] = v;
         }
       }
@@ -501,4 +510,15 @@ __device__ __forceinline__ void xsums_body(const _Float16* x, _Float16* xs, int 
   _Float16* o = xs + mu * 16;
   o[sb] = hi;
   o[8 + sb] = (_Float16)(acc - (float)hi);
+}
+
+// Split-K epilogue: y = sum over the slices' fp32 partials, in slice order.
+template <int YT>
+__device__ __forceinline__ void splitk_reduce_body(const float* part, void* y, int splits, long long mn) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= mn) return;
+  float v = 0.0f;
+  for (int z = 0; z < splits; z++) v += part[z * mn + i];
+  if (YT) ((_Float16*)y)[i] = (_Float16)v;
+  else ((float*)y)[i] = v;
 }

@@ -120,8 +120,9 @@ struct LtArgs {
   const void* x;
   const void* xs;
   void* y;
+  float* part;
   long long row_bytes;
-  int M, N, K, units;
+  int M, N, K, units, usplit;
 };
 struct Gv1Args {
   const void* w;
@@ -148,6 +149,7 @@ struct DeviceModule {
   hipFunction_t gemm[6][2][2] = {};  // K-quant formats only
   hipFunction_t gemm2[6][2][2][2] = {};  // [format][NT-1][MT/8-1][y f16], fp16 x
   hipFunction_t xsums = nullptr;
+  hipFunction_t reduce[2] = {};       // split-K epilogue [y f16]
   hipFunction_t gemv1[6][2] = {};     // [format][y f16]: Q4_K, Q5_K only
   int cus = 0;                        // compute units of the device
 };
@@ -214,6 +216,11 @@ void load_module(DeviceModule& d, int dev) {
         return;
       }
     }
+  }
+  if (hipModuleGetFunction(&d.reduce[0], d.mod, "cq_splitk_reduce_yf32") != hipSuccess ||
+      hipModuleGetFunction(&d.reduce[1], d.mod, "cq_splitk_reduce_yf16") != hipSuccess) {
+    d.err = "missing kernel cq_splitk_reduce_*";
+    return;
   }
   if (hipModuleGetFunction(&d.xsums, d.mod, "cq_xsums_f16") != hipSuccess) {
     d.err = "missing kernel cq_xsums_f16";
@@ -429,6 +436,8 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
   a.N = (int)w->n;
   a.K = (int)w->k;
   a.units = (int)(w->k / 256);
+  a.part = nullptr;
+  a.usplit = a.units;
   int mt = env_int("COMBS_GEMM2_MT", 0);
   if (mt != 8 && mt != 16) mt = m > 128 ? 16 : 8;
   const long long mblk = (m + 16 * mt - 1) / (16 * mt);
@@ -436,26 +445,43 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
   if (nt != 1 && nt != 2) nt = (w->n + 127) / 128 * mblk >= dm->cus ? 2 : 1;
   const long long gx = (w->n + 64 * nt - 1) / (64 * nt);
   if (gx > 0x7fffffffLL || mblk > 65535) return fail(CQ_ERR_BAD_SHAPE, "grid too large");
-  void* ws = nullptr;
-  if (w->format != CQ_Q6_K) {
-    // Stream-ordered scratch for the sums: no state shared between streams,
-    // and recorded as allocation nodes when the stream is being captured.
-    const long long sums = m * a.units * 8;  // one thread per (row, superblock, sub-block)
-    HIP_TRY(hipMallocAsync(&ws, (size_t)sums * 4, s));
-    a.xs = ws;
-    int M = a.M, K = a.K;
-    void* sp[] = {(void*)&x, &ws, &M, &K};
-    hipError_t e = hipModuleLaunchKernel(dm->xsums, (unsigned)((sums + 255) / 256), 1, 1, 256, 1, 1, 0, s, sp, nullptr);
-    if (e != hipSuccess) {
-      (void)hipFreeAsync(ws, s);
-      return fail(CQ_ERR_HIP, "cq_xsums_f16 launch: %s", hipGetErrorString(e));
-    }
+  // Split K when the tiles leave compute units idle (each slice keeps >= 4
+  // superblocks); COMBS_GEMM2_SPLIT forces the slice count.
+  int splits = env_int("COMBS_GEMM2_SPLIT", 0);
+  if (splits < 1) {
+    splits = 1;
+    while (gx * mblk * splits * 2 <= dm->cus && a.units / (splits * 2) >= 4) splits *= 2;
   }
-  void* params[] = {&a};
-  hipError_t e = hipModuleLaunchKernel(dm->gemm2[fi][nt - 1][mt / 8 - 1][yt], (unsigned)gx, (unsigned)mblk, 1, 256, 1,
-                                       1, 0, s, params, nullptr);
+  if (splits > a.units) splits = a.units;
+  a.usplit = (a.units + splits - 1) / splits;
+  splits = (a.units + a.usplit - 1) / a.usplit;
+  // Stream-ordered scratch: activation sums (Q4_K/Q5_K), then split partials.
+  const size_t sums_bytes = w->format != CQ_Q6_K ? (size_t)m * a.units * 32 : 0;
+  const size_t part_bytes = splits > 1 ? (size_t)splits * m * w->n * 4 : 0;
+  void* ws = nullptr;
+  if (sums_bytes + part_bytes) HIP_TRY(hipMallocAsync(&ws, sums_bytes + part_bytes, s));
+  auto launch_all = [&]() -> hipError_t {
+    hipError_t e;
+    if (sums_bytes) {
+      a.xs = ws;
+      const long long sums = m * a.units * 8;  // one thread per (row, superblock, sub-block)
+      int M = a.M, K = a.K;
+      void* sp[] = {(void*)&x, &ws, &M, &K};
+      e = hipModuleLaunchKernel(dm->xsums, (unsigned)((sums + 255) / 256), 1, 1, 256, 1, 1, 0, s, sp, nullptr);
+      if (e != hipSuccess) return e;
+    }
+    if (part_bytes) a.part = (float*)((char*)ws + sums_bytes);
+    void* params[] = {&a};
+    e = hipModuleLaunchKernel(dm->gemm2[fi][nt - 1][mt / 8 - 1][yt], (unsigned)gx, (unsigned)mblk, (unsigned)splits,
+                              256, 1, 1, 0, s, params, nullptr);
+    if (e != hipSuccess || !part_bytes) return e;
+    long long mn = m * w->n;
+    void* rp[] = {&a.part, &y, &splits, &mn};
+    return hipModuleLaunchKernel(dm->reduce[yt], (unsigned)((mn + 255) / 256), 1, 1, 256, 1, 1, 0, s, rp, nullptr);
+  };
+  const hipError_t e = launch_all();
   if (ws) HIP_TRY(hipFreeAsync(ws, s));
-  if (e != hipSuccess) return fail(CQ_ERR_HIP, "cq_gemm2 launch: %s", hipGetErrorString(e));
+  if (e != hipSuccess) return fail(CQ_ERR_HIP, "prefill GEMM launch: %s", hipGetErrorString(e));
   return CQ_OK;
 }
 

@@ -7,6 +7,7 @@
 //   cq_gemm_<fmt>_x<f16|f32>_y<f32|f16>   prefill dequant-GEMM (K-quants)
 //   cq_gemm2_<fmt>_n<1|2>_m<8|16>_y<f32|f16>  prefill dequant-GEMM, large tiles, fp16 x
 //   cq_xsums_f16                          activation sub-block sums for its min term
+//   cq_splitk_reduce_y<f32|f16>           sum of its split-K partials
 //   cq_dequant_<fmt>                      bit-exact dequantisation
 #include "cq_gemv.h"
 #include "cq_gemv1.h"
@@ -87,6 +88,14 @@ GEMM2_KERNEL(cq_gemm2_q6_k_n2_m8_yf32, CQ_Q6_K, 0, 2, 8)
 GEMM2_KERNEL(cq_gemm2_q6_k_n2_m8_yf16, CQ_Q6_K, 1, 2, 8)
 GEMM2_KERNEL(cq_gemm2_q6_k_n2_m16_yf32, CQ_Q6_K, 0, 2, 16)
 GEMM2_KERNEL(cq_gemm2_q6_k_n2_m16_yf16, CQ_Q6_K, 1, 2, 16)
+extern "C" __global__ void __launch_bounds__(256) cq_splitk_reduce_yf32(const float* part, void* y, int splits,
+                                                                       long long mn) {
+  splitk_reduce_body<0>(part, y, splits, mn);
+}
+extern "C" __global__ void __launch_bounds__(256) cq_splitk_reduce_yf16(const float* part, void* y, int splits,
+                                                                       long long mn) {
+  splitk_reduce_body<1>(part, y, splits, mn);
+}
 extern "C" __global__ void __launch_bounds__(256) cq_xsums_f16(const _Float16* x, _Float16* xs, int M, int K) {
   xsums_body(x, xs, M, K);
 }

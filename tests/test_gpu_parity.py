@@ -207,13 +207,15 @@ SCALE_OFF = {QuantFormat.Q4K: (0, 144), QuantFormat.Q5K: (0, 176), QuantFormat.Q
 @pytest.mark.parametrize("fmt", KQ)
 @pytest.mark.parametrize("nt", ["1", "2"])
 @pytest.mark.parametrize("mt", ["8", "16"])
-def test_gemm_scale_edge_cases(cuda, monkeypatch, fmt, nt, mt):
+@pytest.mark.parametrize("split", ["1", "3"])
+def test_gemm_scale_edge_cases(cuda, monkeypatch, fmt, nt, mt, split):
     """Superblocks whose d is zero (min term only), subnormal, or 2^12 times
     larger than their neighbours: the large-tile kernel carries its
     accumulator in units of the running d and must still match the oracle."""
     import torch
     monkeypatch.setenv("COMBS_GEMM2_NT", nt)
     monkeypatch.setenv("COMBS_GEMM2_MT", mt)
+    monkeypatch.setenv("COMBS_GEMM2_SPLIT", split)
     off, bb = SCALE_OFF[fmt]
     n, k, m = 200, 2048, 150
     data = np.frombuffer(synth(fmt, n, k), dtype=np.uint8).copy()
@@ -231,6 +233,40 @@ def test_gemm_scale_edge_cases(cuda, monkeypatch, fmt, nt, mt):
     x = O.x_pattern(m, k, 7, 23, 12.0, 16.0).reshape(m, k)
     print(f"scale edges {fmt.name} nt={nt} mt={mt}", flush=True)
     O.assert_close(_run(w, x, torch.float16, torch.float32, path=L.CQ_PATH_GEMM), O.ref_matmul(x, wd), 1e-3, "gemm")
+
+
+@pytest.mark.parametrize("fmt", KQ)
+@pytest.mark.parametrize("split", ["2", "3", "4"])
+@pytest.mark.parametrize("m", [17, 130])
+def test_gemm_split_k(cuda, monkeypatch, fmt, split, m):
+    """K split over workgroup slices (10 superblocks: 3 slices of 4, 4, 2)
+    with fp32 partials and a reduction kernel, fp32 and fp16 outputs."""
+    import torch
+    monkeypatch.setenv("COMBS_GEMM2_SPLIT", split)
+    n, k = 200, 2560
+    data = synth(fmt, n, k)
+    wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
+    w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
+    x = O.x_pattern(m, k, 11, 29, 14.0, 16.0).reshape(m, k)
+    expect = O.ref_matmul(x, wd)
+    print(f"split-K {fmt.name} split={split} m={m}", flush=True)
+    O.assert_close(_run(w, x, torch.float16, torch.float32, path=L.CQ_PATH_GEMM), expect, 1e-3, "y32")
+    O.assert_close(_run(w, x, torch.float16, torch.float16, path=L.CQ_PATH_GEMM), expect, 1e-3, "y16")
+
+
+@pytest.mark.parametrize("fmt", KQ)
+def test_gemm_split_k_auto_down_projection(cuda, fmt):
+    """A down-projection-like shape (few weight rows, long K) takes the
+    automatic split; checked against float64 torch on the GPU dequant."""
+    import torch
+    rng = np.random.default_rng(11 + int(fmt))
+    n, k, m = 512, 7168, 64
+    data = quantize(fmt, rng.normal(0, 0.02, (n, k)).astype(np.float32))
+    w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
+    wd = torch.from_numpy(dequantize_gpu(fmt, data).reshape(n, k)).cuda().double()
+    x = torch.from_numpy(rng.normal(0, 1, (m, k)).astype(np.float16)).cuda()
+    y = w.matmul_device(x, out_dtype=torch.float32)
+    O.assert_close(y.cpu().numpy(), (x.double() @ wd.t()).cpu().numpy(), 1e-3, "auto split")
 
 
 @pytest.mark.parametrize("fmt", KQ)

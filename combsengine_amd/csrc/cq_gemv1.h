@@ -1,4 +1,5 @@
-// Decode GEMV for a single activation row (m = 1) over K-quant weights:
+// Decode GEMV for a single activation row (m = 1) over K-quant weights
+// (Q4_K, Q5_K, Q6_K):
 // y[n] = sum_k x[k] * W[n, k], streamed at HBM speed.
 //
 // Why not the MFMA GEMV here: with one activation row an MFMA computes 16
@@ -30,7 +31,8 @@
 // Four int8 multiply-adds per instruction (against two per fp16 dot) roughly
 // halve the VALU work per weight, which is what lets the weight stream run
 // at memory speed.
-// Replaces qmatmul.rs:881-930 (Q4_K) and :1064-1117 (Q5_K) for m = 1.
+// Replaces qmatmul.rs:881-930 (Q4_K), :1064-1117 (Q5_K) and :1184-1229
+// (Q6_K) for m = 1.
 #pragma once
 #include "cq_gemv.h"
 
@@ -53,6 +55,7 @@ __shared__ __attribute__((aligned(16))) int8_t gv_xl[GV1_XMAX / 256 * GV1_XSTRID
 __shared__ __attribute__((aligned(16))) int8_t gv_xe[GV1_XMAX / 256 * GV1_XSTRIDE];
 __shared__ float gv_xs[GV1_XMAX / 32];  // s of each 32-value block
 __shared__ float gv_s[GV1_XMAX / 32];   // sum of each 32-value block (fp32 of the fp16 values)
+__shared__ float gv_s16[GV1_XMAX / 16]; // sum of each 16-value half block
 
 // The 8 scales and mins of a K-quant superblock header as floats.
 __device__ __forceinline__ void gv1_scales(const u4v& hd, float sc[8], float mn[8]) {
@@ -69,10 +72,13 @@ __device__ __forceinline__ void gv1_scales(const u4v& hd, float sc[8], float mn[
 template <int FMT>
 struct Gv1Block {
   static constexpr int NC = FmtTraits<FMT>::bytes / 16;
+  static constexpr bool TAIL = FmtTraits<FMT>::bytes % 16 != 0;  // Q6_K: d in the last 2 bytes
   u4v c[NC];
+  uint32_t tail;
   __device__ __forceinline__ void load(const uint8_t* p) {
 #pragma unroll
     for (int i = 0; i < NC; i++) c[i] = ld_u128(p + 16 * i);
+    if (TAIL) tail = ld_u16(p + 16 * NC);
   }
 };
 
@@ -137,6 +143,51 @@ __device__ __forceinline__ float gv1_superblock(const Gv1Block<FMT>& b, const in
   return d * acc - dmin * macc;
 }
 
+__device__ __forceinline__ uint32_t u4_word(const u4v& v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// Q6_K (gguf.rs:968-999): value (half hh, quadrant t, l) is
+// (ql nibble | 2 qh bits << 4) - 32 with scale sc[8hh + l/16 + 2t]; the ql
+// byte is 64hh + 32(t&1) + l (nibble t>>1), the qh byte 32hh + l (bits 2t).
+// The 6-bit q (0..63) goes into v_dot4 as is; the -32 is applied as
+// -32 * sum(x) per 16-value group.  xs16: sums of the unit's 16 groups.
+__device__ __forceinline__ float gv1_superblock_q6k(const Gv1Block<CQ_Q6_K>& b, const int8_t* xh, const int8_t* xl,
+                                                   const int8_t* xe, const float* xs, const float* xs16) {
+  const float d = f16_bits_to_f32(b.tail);
+  const u4v sc0 = b.c[12];
+  const uint32_t scw[4] = {sc0.x, sc0.y, sc0.z, sc0.w};
+  float acc = 0.0f, cacc = 0.0f;
+#pragma unroll
+  for (int hh = 0; hh < 2; hh++) {
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+      int ih[2] = {0, 0}, il[2] = {0, 0}, ie[2] = {0, 0};
+      const int ko = 128 * hh + 32 * t;  // staged byte offset of this quadrant
+#pragma unroll
+      for (int j = 0; j < 8; j++) {   // 4 values l = 4j .. 4j+3
+        const uint32_t qlw = u4_word(b.c[4 * hh + 2 * (t & 1) + (j >> 2)], j & 3);
+        const uint32_t qhw = u4_word(b.c[8 + 2 * hh + (j >> 2)], j & 3);
+        const uint32_t q = ((qlw >> (4 * (t >> 1))) & 0x0F0F0F0Fu) | (((qhw >> (2 * t)) & 0x03030303u) << 4);
+        const int g = j >> 2;  // 16-value group l/16
+        ih[g] = dot4(q, *(const uint32_t*)(xh + ko + 4 * j), ih[g]);
+        il[g] = dot4(q, *(const uint32_t*)(xl + ko + 4 * j), il[g]);
+        ie[g] = dot4(q, *(const uint32_t*)(xe + ko + 4 * j), ie[g]);
+      }
+      const float sblk = xs[4 * hh + t];
+#pragma unroll
+      for (int g = 0; g < 2; g++) {
+        const int si = 8 * hh + g + 2 * t;
+        const float scf = (float)(int8_t)(scw[si >> 2] >> (8 * (si & 3)));
+        const float f = __builtin_fmaf((float)(254 * il[g] + ie[g]), 1.0f / 64516.0f, (float)ih[g]);
+        acc = __builtin_fmaf(scf * sblk, f, acc);
+        cacc = __builtin_fmaf(scf, xs16[8 * hh + 2 * t + g], cacc);
+      }
+    }
+  }
+  return d * __builtin_fmaf(-32.0f, cacc, acc);
+}
+
 template <int FMT, int YT>
 __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
   constexpr int BB = FmtTraits<FMT>::bytes;
@@ -192,6 +243,7 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
     mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
     sm += __shfl_xor(sm, 1, 64);
+    const float sm16 = sm;  // this thread pair's 16 values
     sm += __shfl_xor(sm, 2, 64);
     const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
     uint32_t hw[2] = {0, 0}, lw[2] = {0, 0}, ew[2] = {0, 0};
@@ -217,6 +269,7 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
         gv_xs[c >> 2] = mx * (1.0f / 127.0f);
         gv_s[c >> 2] = sm;
       }
+      if ((c & 1) == 0) gv_s16[c >> 1] = sm16;
     }
   }
   __syncthreads();
@@ -225,9 +278,13 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
     const int r0 = tt * a.rows;
     const int nrows = min(a.rows, a.N - r0);
     float part = 0.0f;
-    if (lane < lanes_used && myrow < nrows)
-      part = gv1_superblock<FMT>(blk, gv_xh + myunit * GV1_XSTRIDE, gv_xl + myunit * GV1_XSTRIDE,
-                                 gv_xe + myunit * GV1_XSTRIDE, gv_xs + 8 * myunit, gv_s + 8 * myunit);
+    if (lane < lanes_used && myrow < nrows) {
+      const int8_t* xh = gv_xh + myunit * GV1_XSTRIDE;
+      const int8_t* xl = gv_xl + myunit * GV1_XSTRIDE;
+      const int8_t* xe = gv_xe + myunit * GV1_XSTRIDE;
+      if constexpr (FMT == CQ_Q6_K) part = gv1_superblock_q6k(blk, xh, xl, xe, gv_xs + 8 * myunit, gv_s16 + 16 * myunit);
+      else part = gv1_superblock<FMT>(blk, xh, xl, xe, gv_xs + 8 * myunit, gv_s + 8 * myunit);
+    }
     if ((a.units & (a.units - 1)) == 0) {
       // a row's lanes form an aligned group of `units` lanes: butterfly within it
       for (int o = a.units >> 1; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);

@@ -108,3 +108,5 @@ GEMV1_KERNEL(cq_gemv1_q4_k_yf32, CQ_Q4_K, 0)
 GEMV1_KERNEL(cq_gemv1_q4_k_yf16, CQ_Q4_K, 1)
 GEMV1_KERNEL(cq_gemv1_q5_k_yf32, CQ_Q5_K, 0)
 GEMV1_KERNEL(cq_gemv1_q5_k_yf16, CQ_Q5_K, 1)
+GEMV1_KERNEL(cq_gemv1_q6_k_yf32, CQ_Q6_K, 0)
+GEMV1_KERNEL(cq_gemv1_q6_k_yf16, CQ_Q6_K, 1)

@@ -159,7 +159,7 @@ def test_gemv_large_and_ragged(cuda, fmt, n, k, m):
 KQ = [QuantFormat.Q4K, QuantFormat.Q5K, QuantFormat.Q6K]
 
 
-@pytest.mark.parametrize("fmt", [QuantFormat.Q4K, QuantFormat.Q5K])
+@pytest.mark.parametrize("fmt", KQ)
 @pytest.mark.parametrize("n,k", [(300, 4096), (35, 512), (97, 3584), (50, 5120), (70, 14336), (130, 16384), (1, 256)])
 @pytest.mark.parametrize("gemv1", ["1", "0"])
 def test_gemv_single_row(cuda, monkeypatch, fmt, n, k, gemv1):

@@ -1,5 +1,5 @@
-// Decode GEMV for a single activation row (m = 1) over K-quant weights
-// (Q4_K, Q5_K, Q6_K):
+// Decode GEMV for a single activation row (m = 1), every format (K-quant
+// superblocks; legacy blocks eight at a time):
 // y[n] = sum_k x[k] * W[n, k], streamed at HBM speed.
 //
 // Why not the MFMA GEMV here: with one activation row an MFMA computes 16
@@ -31,8 +31,8 @@
 // Four int8 multiply-adds per instruction (against two per fp16 dot) roughly
 // halve the VALU work per weight, which is what lets the weight stream run
 // at memory speed.
-// Replaces qmatmul.rs:881-930 (Q4_K), :1064-1117 (Q5_K) and :1184-1229
-// (Q6_K) for m = 1.
+// Replaces qmatmul.rs:92-125 (Q4_0), :386-423 (Q5_0), :440-470 (Q8_0),
+// :881-930 (Q4_K), :1064-1117 (Q5_K) and :1184-1229 (Q6_K) for m = 1.
 #pragma once
 #include "cq_gemv.h"
 
@@ -68,11 +68,19 @@ __device__ __forceinline__ void gv1_scales(const u4v& hd, float sc[8], float mn[
   }
 }
 
-// One superblock in registers, as 16-byte chunks.
+// Bytes of a lane's unit of 256 values: one K-quant superblock, or eight
+// consecutive 32-value blocks of a legacy format (144 / 176 / 272 bytes, so
+// units stay 16-byte aligned whenever rows are).
+template <int FMT>
+constexpr int gv1_unit_bytes() {
+  return FmtTraits<FMT>::vals == 256 ? FmtTraits<FMT>::bytes : 8 * (FmtTraits<FMT>::bytes / LB);
+}
+
+// One unit in registers, as 16-byte chunks.
 template <int FMT>
 struct Gv1Block {
-  static constexpr int NC = FmtTraits<FMT>::bytes / 16;
-  static constexpr bool TAIL = FmtTraits<FMT>::bytes % 16 != 0;  // Q6_K: d in the last 2 bytes
+  static constexpr int NC = gv1_unit_bytes<FMT>() / 16;
+  static constexpr bool TAIL = gv1_unit_bytes<FMT>() % 16 != 0;  // Q6_K: d in the last 2 bytes
   u4v c[NC];
   uint32_t tail;
   __device__ __forceinline__ void load(const uint8_t* p) {
@@ -188,9 +196,79 @@ __device__ __forceinline__ float gv1_superblock_q6k(const Gv1Block<CQ_Q6_K>& b, 
   return d * __builtin_fmaf(-32.0f, cacc, acc);
 }
 
+// 32-bit word at even byte offset o of a unit in registers (o is a
+// compile-time constant once unrolled; odd halfword offsets cost one
+// v_alignbit).
+template <int NC>
+__device__ __forceinline__ uint32_t gv1_word(const u4v (&c)[NC], int o) {
+  const int wi = o >> 2;
+  const uint32_t w0 = u4_word(c[wi >> 2], wi & 3);
+  if ((o & 3) == 0) return w0;
+  const uint32_t w1 = u4_word(c[(wi + 1) >> 2], (wi + 1) & 3);
+  return __builtin_amdgcn_alignbit(w1, w0, 16);
+}
+template <int NC>
+__device__ __forceinline__ uint32_t gv1_half(const u4v (&c)[NC], int o) {
+  const int wi = o >> 2;
+  return (u4_word(c[wi >> 2], wi & 3) >> (8 * (o & 2))) & 0xFFFFu;
+}
+
+// Legacy 32-value blocks, eight per unit (block b = values 32b .. 32b+31):
+// Q4_0 (gguf.rs:755-774) value j = low nibble of qs byte j, j + 16 = its high
+// nibble, (q - 8) * d; Q5_0 (gguf.rs:825-847) adds qh bit j / j + 16 as the
+// 5th bit, (q - 16) * d; Q8_0 (gguf.rs:779-794) q = signed byte j, q * d.
+// The offsets -8 / -16 are applied as -8 / -16 * sum(x) of the block.
+template <int FMT>
+__device__ __forceinline__ float gv1_unit_legacy(const Gv1Block<FMT>& b, const int8_t* xh, const int8_t* xl,
+                                                 const int8_t* xe, const float* xs, const float* su) {
+  constexpr int BB = FmtTraits<FMT>::bytes / LB;  // bytes per 32-value block
+  float acc = 0.0f;
+#pragma unroll
+  for (int blk = 0; blk < 8; blk++) {
+    const int o = BB * blk;
+    const float d = f16_bits_to_f32(gv1_half(b.c, o));
+    int ih = 0, il = 0, ie = 0;
+    const int xo = 32 * blk;
+    if constexpr (FMT == CQ_Q8_0) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const uint32_t q = gv1_word(b.c, o + 2 + 4 * i);
+        ih = dot4(q, *(const uint32_t*)(xh + xo + 4 * i), ih);
+        il = dot4(q, *(const uint32_t*)(xl + xo + 4 * i), il);
+        ie = dot4(q, *(const uint32_t*)(xe + xo + 4 * i), ie);
+      }
+    } else {
+      constexpr int QO = FMT == CQ_Q5_0 ? 6 : 2;  // qs offset in the block
+      uint32_t qh = 0;
+      if constexpr (FMT == CQ_Q5_0) qh = gv1_word(b.c, o + 2);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t w = gv1_word(b.c, o + QO + 4 * i);
+        uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+        if constexpr (FMT == CQ_Q5_0) {
+          lo |= spread4(qh >> (4 * i)) << 4;
+          hi |= spread4(qh >> (16 + 4 * i)) << 4;
+        }
+        ih = dot4(lo, *(const uint32_t*)(xh + xo + 4 * i), ih);
+        il = dot4(lo, *(const uint32_t*)(xl + xo + 4 * i), il);
+        ie = dot4(lo, *(const uint32_t*)(xe + xo + 4 * i), ie);
+        ih = dot4(hi, *(const uint32_t*)(xh + xo + 16 + 4 * i), ih);
+        il = dot4(hi, *(const uint32_t*)(xl + xo + 16 + 4 * i), il);
+        ie = dot4(hi, *(const uint32_t*)(xe + xo + 16 + 4 * i), ie);
+      }
+    }
+    const float f = __builtin_fmaf((float)(254 * il + ie), 1.0f / 64516.0f, (float)ih);
+    float v = xs[blk] * f;
+    if constexpr (FMT == CQ_Q4_0) v = __builtin_fmaf(-8.0f, su[blk], v);
+    if constexpr (FMT == CQ_Q5_0) v = __builtin_fmaf(-16.0f, su[blk], v);
+    acc = __builtin_fmaf(d, v, acc);
+  }
+  return acc;
+}
+
 template <int FMT, int YT>
 __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
-  constexpr int BB = FmtTraits<FMT>::bytes;
+  constexpr int BB = gv1_unit_bytes<FMT>();
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lanes_used = a.rows * a.units;
@@ -283,6 +361,8 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
       const int8_t* xl = gv_xl + myunit * GV1_XSTRIDE;
       const int8_t* xe = gv_xe + myunit * GV1_XSTRIDE;
       if constexpr (FMT == CQ_Q6_K) part = gv1_superblock_q6k(blk, xh, xl, xe, gv_xs + 8 * myunit, gv_s16 + 16 * myunit);
+      else if constexpr (FmtTraits<FMT>::vals != 256)
+        part = gv1_unit_legacy<FMT>(blk, xh, xl, xe, gv_xs + 8 * myunit, gv_s + 8 * myunit);
       else part = gv1_superblock<FMT>(blk, xh, xl, xe, gv_xs + 8 * myunit, gv_s + 8 * myunit);
     }
     if ((a.units & (a.units - 1)) == 0) {

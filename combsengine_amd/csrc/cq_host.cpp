@@ -150,7 +150,7 @@ struct DeviceModule {
   hipFunction_t gemm2[6][2][2][2] = {};  // [format][NT-1][MT/8-1][y f16], fp16 x
   hipFunction_t xsums = nullptr;
   hipFunction_t reduce[2] = {};       // split-K epilogue [y f16]
-  hipFunction_t gemv1[6][2] = {};     // [format][y f16]: K-quants
+  hipFunction_t gemv1[6][2] = {};     // [format][y f16]
   int cus = 0;                        // compute units of the device
 };
 DeviceModule g_dev[kMaxDevices];
@@ -208,7 +208,6 @@ void load_module(DeviceModule& d, int dev) {
     }
   }
   for (int fi = 0; fi < 6; fi++) {
-    if (block_values(kFormats[fi]) != 256) continue;
     for (int yt = 0; yt < 2; yt++) {
       snprintf(name, sizeof name, "cq_gemv1_%s_y%s", fmt_name(kFormats[fi]), yt ? "f16" : "f32");
       if (hipModuleGetFunction(&d.gemv1[fi][yt], d.mod, name) != hipSuccess) {
@@ -390,12 +389,12 @@ static cq_status launch_gemv(DeviceModule* dm, const cq_weight* w, const void* x
   return CQ_OK;
 }
 
-// Decode GEMV for one fp16 activation row (cq_gemv1_*, K-quants): wave
-// tasks of max(1, 64/units) whole rows, a persistent grid of one 4-wave
+// Decode GEMV for one fp16 activation row (cq_gemv1_*, every format, K a
+// multiple of 256): wave tasks of max(1, 64/units) whole rows of 256-value units, a persistent grid of one 4-wave
 // workgroup per compute unit.  Returns false when the shape is not covered.
 constexpr int kGv1Waves = 4, kGv1MaxK = 16384;
 static bool gemv1_fits(const cq_weight* w) {
-  return block_values(w->format) == 256 && w->k <= kGv1MaxK && w->k / 256 <= 64;
+  return w->k % 256 == 0 && w->k <= kGv1MaxK && w->k / 256 <= 64;
 }
 static cq_status launch_gemv1(DeviceModule* dm, const cq_weight* w, const void* x, void* y, int yt, hipStream_t s) {
   const int fi = fmt_index(w->format);

@@ -3,7 +3,7 @@
 // hipModuleLoadData.  Kernel names are extern "C" so the host can look them
 // up with hipModuleGetFunction:
 //   cq_gemv_<fmt>_x<f16|f32>_y<f32|f16>   decode GEMV (m-tiles of 16)
-//   cq_gemv1_<fmt>_y<f32|f16>             decode GEMV, one fp16 activation row, K-quants
+//   cq_gemv1_<fmt>_y<f32|f16>             decode GEMV, one fp16 activation row
 //   cq_gemm_<fmt>_x<f16|f32>_y<f32|f16>   prefill dequant-GEMM (K-quants)
 //   cq_gemm2_<fmt>_n<1|2>_m<8|16>_y<f32|f16>  prefill dequant-GEMM, large tiles, fp16 x
 //   cq_xsums_f16                          activation sub-block sums for its min term
@@ -110,3 +110,9 @@ GEMV1_KERNEL(cq_gemv1_q5_k_yf32, CQ_Q5_K, 0)
 GEMV1_KERNEL(cq_gemv1_q5_k_yf16, CQ_Q5_K, 1)
 GEMV1_KERNEL(cq_gemv1_q6_k_yf32, CQ_Q6_K, 0)
 GEMV1_KERNEL(cq_gemv1_q6_k_yf16, CQ_Q6_K, 1)
+GEMV1_KERNEL(cq_gemv1_q4_0_yf32, CQ_Q4_0, 0)
+GEMV1_KERNEL(cq_gemv1_q4_0_yf16, CQ_Q4_0, 1)
+GEMV1_KERNEL(cq_gemv1_q5_0_yf32, CQ_Q5_0, 0)
+GEMV1_KERNEL(cq_gemv1_q5_0_yf16, CQ_Q5_0, 1)
+GEMV1_KERNEL(cq_gemv1_q8_0_yf32, CQ_Q8_0, 0)
+GEMV1_KERNEL(cq_gemv1_q8_0_yf16, CQ_Q8_0, 1)

@@ -39,15 +39,16 @@ def algo_bytes(wbytes, m, k, n, xbytes=2, ybytes=4):
     return wbytes + m * k * xbytes + m * n * ybytes
 
 
-def make_pool(fmt, n, k, pool_bytes, seed):
-    """One seeded quantised weight, replicated into distinct device buffers."""
+def make_pool(fmt, n, k, pool_bytes, seed, count=None):
+    """One seeded quantised weight, replicated into distinct device buffers
+    (`count` of them, or as many as fit in `pool_bytes`)."""
     import numpy as np
     import torch
     from combsengine_amd import QuantWeight, quantize
     rng = np.random.default_rng(seed)
     data = np.frombuffer(quantize(fmt, rng.normal(0, 0.02, (n, k)).astype(np.float32)), np.uint8)
     base = torch.from_numpy(data.copy()).cuda()
-    count = max(1, int(pool_bytes // data.size))
+    count = count or max(1, int(pool_bytes // data.size))
     pool = [QuantWeight.from_device(fmt, base if i == 0 else base.clone(), n, k) for i in range(count)]
     return pool, data
 

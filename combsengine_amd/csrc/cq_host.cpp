@@ -446,7 +446,12 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
   if (gx > 0x7fffffffLL || mblk > 65535) return fail(CQ_ERR_BAD_SHAPE, "grid too large");
   // Split K when the tiles leave compute units idle (each slice keeps >= 4
   // superblocks); COMBS_GEMM2_SPLIT forces the slice count.
-  int splits = env_int("COMBS_GEMM2_SPLIT", 0);
+  // Not while the stream is being captured into a graph: split-K inside a
+  // captured graph has not been verified on the GPU, so captured launches
+  // take the unsplit path.
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(s, &cs));
+  int splits = cs == hipStreamCaptureStatusNone ? env_int("COMBS_GEMM2_SPLIT", 0) : 1;
   if (splits < 1) {
     splits = 1;
     while (gx * mblk * splits * 2 <= dm->cus && a.units / (splits * 2) >= 4) splits *= 2;

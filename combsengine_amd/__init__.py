@@ -11,3 +11,4 @@ from .qlinear import (  # noqa: F401
     BadShape, Linear, ModelError, QuantFormat, QuantLinearOp, QuantTensor, QuantWeight,
     block_bytes, block_values, dequantize_gpu, quantize, tensor_byte_size, try_quant_linear,
 )
+from .gguf import GgufSource  # noqa: F401,E402

@@ -36,7 +36,6 @@
 #pragma once
 #include "cq_gemv.h"
 
-#define GV1_WAVES 4
 #define GV1_XMAX 16384                       // largest K staged
 #define GV1_XSTRIDE 272                      // bytes per staged 256-value unit (16 pad)
 
@@ -266,14 +265,22 @@ __device__ __forceinline__ float gv1_unit_legacy(const Gv1Block<FMT>& b, const i
   return acc;
 }
 
+// Waves per workgroup: 8 (two per SIMD) where the register budget allows it
+// without spilling (Q4_K / Q5_K), else 4.
+template <int FMT>
+constexpr int gv1_waves() {
+  return FMT == CQ_Q4_K || FMT == CQ_Q5_K ? 8 : 4;
+}
+
 template <int FMT, int YT>
 __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
+  constexpr int NW = gv1_waves<FMT>();
   constexpr int BB = gv1_unit_bytes<FMT>();
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lanes_used = a.rows * a.units;
   const int myrow = lane / a.units, myunit = lane - myrow * a.units;
-  const int stride = gridDim.x * GV1_WAVES;
+  const int stride = gridDim.x * NW;
   // lane's superblock of task t (lanes past the task's rows reread its first)
   auto block_ptr = [&](int t) {
     const int r0 = t * a.rows;
@@ -283,7 +290,7 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
   // Load order matters (the vector-memory counter retires in order): the
   // activation chunks first, then the first task's weights, so that staging
   // x into LDS waits only for x while the weights' HBM latency runs on.
-  constexpr int XL = GV1_XMAX / 8 / (64 * GV1_WAVES);  // 16-byte x chunks per thread, at most
+  constexpr int XL = GV1_XMAX / 8 / (64 * NW);  // 16-byte x chunks per thread, at most
   u4v xv[XL];
   // (Branch-free: indices past the end are clamped, so chunks may be loaded
   // and stored twice with the same value; control-flow joins would make the
@@ -291,10 +298,10 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
   const int xc_last = a.K / 8 - 1;
 #pragma unroll
   for (int i = 0; i < XL; i++) {
-    const int c = min((int)threadIdx.x + 64 * GV1_WAVES * i, xc_last);
+    const int c = min((int)threadIdx.x + 64 * NW * i, xc_last);
     xv[i] = ld_u128((const uint8_t*)(a.x + 8 * c));
   }
-  int t = blockIdx.x * GV1_WAVES + wave;
+  int t = blockIdx.x * NW + wave;
   Gv1Block<FMT> cur, nxt;
   cur.load(block_ptr(min(t, a.tasks - 1)));
   __builtin_amdgcn_sched_barrier(0);  // keep the weight loads ahead of the staging
@@ -303,8 +310,8 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
   // last chunk and store nothing.
 #pragma unroll
   for (int i = 0; i < XL; i++) {
-    if (64 * GV1_WAVES * i > xc_last) break;  // uniform
-    const int craw = (int)threadIdx.x + 64 * GV1_WAVES * i;
+    if (64 * NW * i > xc_last) break;  // uniform
+    const int craw = (int)threadIdx.x + 64 * NW * i;
     const int c = min(craw, xc_last);
     const uint32_t wv[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
     float v[8], mx = 0.0f, sm = 0.0f;

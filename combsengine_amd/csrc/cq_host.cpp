@@ -390,9 +390,11 @@ static cq_status launch_gemv(DeviceModule* dm, const cq_weight* w, const void* x
 }
 
 // Decode GEMV for one fp16 activation row (cq_gemv1_*, every format, K a
-// multiple of 256): wave tasks of max(1, 64/units) whole rows of 256-value units, a persistent grid of one 4-wave
-// workgroup per compute unit.  Returns false when the shape is not covered.
-constexpr int kGv1Waves = 4, kGv1MaxK = 16384;
+// multiple of 256): wave tasks of max(1, 64/units) whole rows of 256-value
+// units, a persistent grid of one workgroup (8 or 4 waves) per compute unit.  Returns false when the shape is not covered.
+constexpr int kGv1MaxK = 16384;
+// Waves per cq_gemv1 workgroup (the kernels' launch bounds).
+static int gemv1_waves(int format) { return format == CQ_Q4_K || format == CQ_Q5_K ? 8 : 4; }
 static bool gemv1_fits(const cq_weight* w) {
   return w->k % 256 == 0 && w->k <= kGv1MaxK && w->k / 256 <= 64;
 }
@@ -408,12 +410,13 @@ static cq_status launch_gemv1(DeviceModule* dm, const cq_weight* w, const void* 
   a.units = (int)(w->k / 256);
   a.rows = a.units >= 64 ? 1 : 64 / a.units;
   a.tasks = (int)((w->n + a.rows - 1) / a.rows);
-  const int wgs = (a.tasks + kGv1Waves - 1) / kGv1Waves;
+  const int nw = gemv1_waves(w->format);
+  const int wgs = (a.tasks + nw - 1) / nw;
   int cap = env_int("COMBS_GEMV1_GRID", dm->cus);
   if (cap < 1) cap = 1;
   const int grid = wgs < cap ? wgs : cap;
   void* params[] = {&a};
-  HIP_TRY(hipModuleLaunchKernel(dm->gemv1[fi][yt], (unsigned)grid, 1, 1, 64 * kGv1Waves, 1, 1, 0, s, params, nullptr));
+  HIP_TRY(hipModuleLaunchKernel(dm->gemv1[fi][yt], (unsigned)grid, 1, 1, 64 * nw, 1, 1, 0, s, params, nullptr));
   return CQ_OK;
 }
 

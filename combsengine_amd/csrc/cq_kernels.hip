@@ -101,7 +101,7 @@ extern "C" __global__ void __launch_bounds__(256) cq_xsums_f16(const _Float16* x
 }
 
 #define GEMV1_KERNEL(NAME, FMT, YT)                                                    \
-  extern "C" __global__ void __launch_bounds__(64 * GV1_WAVES) NAME(const Gv1Args a) { \
+  extern "C" __global__ void __launch_bounds__(64 * gv1_waves<FMT>()) NAME(const Gv1Args a) { \
     gemv1_body<FMT, YT>(a);                                                            \
   }
 GEMV1_KERNEL(cq_gemv1_q4_k_yf32, CQ_Q4_K, 0)

@@ -70,8 +70,11 @@ __shared__ __attribute__((aligned(16))) _Float16 lt_s1[16 * LT_MAXMT * 16];
 // 16-byte chunk c (0..15) of a staged row holds K values [8c, 8c+8) of the
 // step.  MFMA step s, lane group g reads chunk lt_chunk; within each 32-lane
 // half of the wave the chunks differ in one bit only (bit 1 for Q4_K/Q5_K,
-// bit 2 for Q6_K), and the row swizzle lt_sw (XOR over the other three bits)
-// spreads the 8 rows of either parity across them.
+// bit 2 for Q6_K).  The row swizzle lt_sw XORs that bit with the row's
+// parity and the other three bits with the rest of the row index, so that
+// both the 16 lanes of one lane group (16 rows, one 256-byte window of bank
+// groups) and the 32 lanes of a half wave (two groups, a 512-byte window)
+// hit distinct 16-byte bank groups.
 template <int FMT>
 __device__ __forceinline__ int lt_chunk(int g, int s) {
   if (FMT == CQ_Q6_K) return 8 * (s >> 1) + 4 * (g & 1) + 2 * (g >> 1) + (s & 1);
@@ -79,9 +82,9 @@ __device__ __forceinline__ int lt_chunk(int g, int s) {
 }
 template <int FMT>
 __device__ __forceinline__ int lt_sw(int r) {
-  const int jj = (r & 15) >> 1;
-  if (FMT == CQ_Q6_K) return (jj & 3) | ((jj & 4) << 1);
-  return (jj & 1) | ((jj & 6) << 1);
+  const int jj = (r & 15) >> 1, p = r & 1;
+  if (FMT == CQ_Q6_K) return (p << 2) | (jj & 3) | ((jj & 4) << 1);
+  return (p << 1) | (jj & 1) | ((jj & 6) << 1);
 }
 
 // Packed bytes of one half superblock (step) for lane (row j, group g).
@@ -291,11 +294,15 @@ struct LtGemm {
 #pragma unroll
     for (int t = 0; t < NT; t++) r[t] = prep<H>(t);
     const char* xr = (const char*)(X + j * LT_KC);
-    // A fragments: one register set, each reloaded for step s+1 right after
-    // its step-s MFMAs have been issued (MT * NT MFMAs of latency cover).
-    h8 av[MT];
+    // A fragments: a ring of MT/2 registers.  Tile tm's fragment of step s
+    // sits in slot tm % (MT/2); once its MFMAs are issued the slot is
+    // reloaded with the fragment needed MT/2 tiles later (tile tm + MT/2 of
+    // this step, or tile tm - MT/2 of the next), MT MFMAs ahead of its use.
+    constexpr int HR = MT / 2;
+    auto afrag = [&](int s, int tm) { return *(const h8*)(xr + tm * 16 * LT_KC * 2 + acol[s]); };
+    h8 av[HR];
 #pragma unroll
-    for (int tm = 0; tm < MT; tm++) av[tm] = *(const h8*)(xr + tm * 16 * LT_KC * 2 + acol[0]);
+    for (int i = 0; i < HR; i++) av[i] = afrag(0, i);
     h8 bsave[2][NT];  // Q4_K: high-nibble operands of steps 2, 3
 #pragma unroll
     for (int s = 0; s < 4; s++) {
@@ -312,23 +319,21 @@ struct LtGemm {
       }
 #pragma unroll
       for (int tm = 0; tm < MT; tm++) {
+        const int slot = tm % HR;
 #pragma unroll
         for (int t = 0; t < NT; t++) {
           if (H == 0 && s == 0) {
 #pragma unroll
             for (int q = 0; q < 4; q++) acc[t][tm][q] *= r[t];
           }
-          acc[t][tm] = mfma(av[tm], b[t], acc[t][tm]);
+          acc[t][tm] = mfma(av[slot], b[t], acc[t][tm]);
         }
-        if (!Q6 && s < 3) av[tm] = *(const h8*)(xr + tm * 16 * LT_KC * 2 + acol[s + 1]);
-      }
-      if constexpr (Q6) {
+        if constexpr (Q6) {
 #pragma unroll
-        for (int tm = 0; tm < MT; tm++) {
-#pragma unroll
-          for (int t = 0; t < NT; t++) acc[t][tm] = mfma(av[tm], bl[t], acc[t][tm]);
-          if (s < 3) av[tm] = *(const h8*)(xr + tm * 16 * LT_KC * 2 + acol[s + 1]);
+          for (int t = 0; t < NT; t++) acc[t][tm] = mfma(av[slot], bl[t], acc[t][tm]);
         }
+        if (tm < HR) av[slot] = afrag(s, tm + HR);
+        else if (s < 3) av[slot] = afrag(s + 1, tm - HR);
       }
       // keep each step's decode next to its MFMAs
       __builtin_amdgcn_sched_barrier(0);

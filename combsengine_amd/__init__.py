@@ -8,7 +8,7 @@ dequantised inside hand-written HIP kernels for gfx950 behind a C ABI
 reference's seam; the compute lives only in lib/libcombs_qlinear.so.
 """
 from .qlinear import (  # noqa: F401
-    BadShape, Linear, ModelError, QuantFormat, QuantLinearOp, QuantTensor, QuantWeight,
+    Activation, BadShape, Linear, ModelError, QuantFormat, QuantLinearOp, QuantTensor, QuantWeight, gated_up,
     block_bytes, block_values, dequantize_gpu, quantize, tensor_byte_size, try_quant_linear,
 )
 from .gguf import GgufSource  # noqa: F401,E402

@@ -14,13 +14,15 @@ LIB_PATH = os.path.join(HERE, "lib", "libcombs_qlinear.so")
 EXPORTS = (
     "cq_block_values", "cq_block_bytes", "cq_tensor_bytes", "cq_weight_create",
     "cq_weight_wrap_device", "cq_weight_destroy", "cq_weight_dims", "cq_weight_vram_bytes",
-    "cq_weight_device_ptr", "cq_matmul", "cq_matmul_path", "cq_dequantize", "cq_quantize",
+    "cq_weight_device_ptr", "cq_matmul", "cq_matmul_path", "cq_matmul_bias", "cq_matmul_gate_up",
+    "cq_dequantize", "cq_quantize",
     "cq_last_error", "cq_version",
 )
 
 CQ_OK, CQ_ERR_BAD_FORMAT, CQ_ERR_BAD_SHAPE, CQ_ERR_BAD_DTYPE, CQ_ERR_NULL, CQ_ERR_HIP, CQ_ERR_NO_DEVICE = range(7)
 CQ_F32, CQ_F16 = 0, 1
 CQ_PATH_AUTO, CQ_PATH_GEMV, CQ_PATH_GEMM = 0, 1, 2
+CQ_ACT_SILU, CQ_ACT_GELU_TANH, CQ_ACT_GELU = 0, 1, 2
 
 _lib = None
 
@@ -51,6 +53,8 @@ def lib():
         "cq_weight_device_ptr": ([P], P),
         "cq_matmul": ([P, P, i32, i64, P, i32, P], i32),
         "cq_matmul_path": ([P, P, i32, i64, P, i32, i32, P], i32),
+        "cq_matmul_bias": ([P, P, i32, i64, P, i32, P, i32, P], i32),
+        "cq_matmul_gate_up": ([P, P, P, i32, i64, i32, P, i32, P], i32),
         "cq_dequantize": ([i32, P, sz, i64, P, P], i32),
         "cq_quantize": ([i32, P, i64, i64, P, sz, i32], i32),
         "cq_last_error": ([], ctypes.c_char_p),

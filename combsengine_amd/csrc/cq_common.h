@@ -8,6 +8,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include "cq_epi.h"
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -144,4 +145,36 @@ __device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, ui
     sc = (b2 & 0x0F) | ((b0 >> 6) << 4);
     mn = (b2 >> 4) | ((b1 >> 6) << 4);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Output epilogue (CqEpi): v = acc (+ bias[n]); with aux, v = act(v) * aux[i].
+// SiLU is v * sigmoid(v) (burn's silu); the tanh GELU is
+// 0.5 v (1 + tanh(u)), u = sqrt(2/pi) (v + 0.044715 v^3), evaluated through
+// the identity 0.5 (1 + tanh(u)) = sigmoid(2u); the exact GELU is
+// 0.5 v (1 + erf(v / sqrt(2))).
+__device__ __forceinline__ float cq_sigmoid(float z) { return 1.0f / (1.0f + __expf(-z)); }
+__device__ __forceinline__ float cq_act(float v, int act) {
+  if (act == CQ_EPI_ACT_SILU) return v * cq_sigmoid(v);
+  if (act == CQ_EPI_ACT_GELU_TANH) {
+    const float u = 0.7978845608028654f * (v + 0.044715f * v * v * v);
+    return v * cq_sigmoid(2.0f * u);
+  }
+  return 0.5f * v * (1.0f + erff(v * 0.7071067811865476f));
+}
+// idx: flat index of the output element [m][n]; n: its column.
+__device__ __forceinline__ float cq_epilogue(const CqEpi& e, float v, size_t idx, int n) {
+  if (e.bias) v += e.bias_f16 ? (float)((const _Float16*)e.bias)[n] : ((const float*)e.bias)[n];
+  if (e.aux) {
+    const float u = e.aux_f16 ? (float)((const _Float16*)e.aux)[idx] : ((const float*)e.aux)[idx];
+    v = cq_act(v, e.act) * u;
+  }
+  return v;
+}
+// Stores one output element through the epilogue.
+template <int YT>
+__device__ __forceinline__ void cq_store(void* y, const CqEpi& e, float v, size_t idx, int n) {
+  v = cq_epilogue(e, v, idx, n);
+  if (YT) ((_Float16*)y)[idx] = (_Float16)v;
+  else ((float*)y)[idx] = v;
 }

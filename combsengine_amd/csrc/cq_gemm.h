@@ -27,6 +27,7 @@ struct GemmArgs {
   long long row_bytes;
   int M, N, K;
   int units;  // superblocks per row
+  CqEpi epi;
 };
 
 #define GM_KC 256           // K values per step (one superblock)
@@ -230,10 +231,7 @@ __device__ __forceinline__ void gemm_body(const GemmArgs& a) {
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const int m = m0 + 16 * t + 4 * g + r, n = n0 + j;
-      if (m < a.M && n < a.N) {
-        if (YT) ((_Float16*)a.y)[(size_t)m * a.N + n] = (_Float16)acc[t][r];
-        else ((float*)a.y)[(size_t)m * a.N + n] = acc[t][r];
-      }
+      if (m < a.M && n < a.N) cq_store<YT>(a.y, a.epi, acc[t][r], (size_t)m * a.N + n, n);
     }
   }
 }

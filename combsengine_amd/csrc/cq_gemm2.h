@@ -58,6 +58,7 @@ struct LtArgs {
   long long row_bytes;
   int M, N, K, units;  // units = K / 256
   int usplit;          // superblocks per K slice (blockIdx.z); units when not split
+  CqEpi epi;           // applied here, or by the split-K reduction
 };
 
 // Distinct static arrays: the compiler can then see that reading one buffer
@@ -479,8 +480,7 @@ __device__ __forceinline__ void gemm2_body(const LtArgs& a) {
         if (m < a.M && n < a.N) {
           const float v = s.deff[t] * s.acc[t][tm][r];
           if (a.part) a.part[((size_t)blockIdx.z * a.M + m) * a.N + n] = v;
-          else if (YT) ((_Float16*)a.y)[(size_t)m * a.N + n] = (_Float16)v;
-          else ((float*)a.y)[(size_t)m * a.N + n] = v;
+          else cq_store<YT>(a.y, a.epi, v, (size_t)m * a.N + n, n);
         }
       }
     }
@@ -519,11 +519,11 @@ __device__ __forceinline__ void xsums_body(const _Float16* x, _Float16* xs, int 
 
 // Split-K epilogue: y = sum over the slices' fp32 partials, in slice order.
 template <int YT>
-__device__ __forceinline__ void splitk_reduce_body(const float* part, void* y, int splits, long long mn) {
+__device__ __forceinline__ void splitk_reduce_body(const float* part, void* y, int splits, long long mn, int N,
+                                                   CqEpi epi) {
   const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= mn) return;
   float v = 0.0f;
   for (int z = 0; z < splits; z++) v += part[z * mn + i];
-  if (YT) ((_Float16*)y)[i] = (_Float16)v;
-  else ((float*)y)[i] = v;
+  cq_store<YT>(y, epi, v, (size_t)i, (int)(i % N));
 }

@@ -30,6 +30,7 @@ struct GemvArgs {
   int units;          // work units per row
   int kc;             // K values per LDS chunk of activations (multiple of a unit)
   int lds_stride;     // halves per staged activation row (kc + 8)
+  CqEpi epi;
 };
 
 // Byte selectors for v_perm_b32(hi, lo, sel): byte i of the result takes
@@ -579,19 +580,13 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a) {
       float s = red[0][r][ln];
       for (int w2 = 1; w2 < nw; w2++) s += red[w2][r][ln];
       const int m = m0 + 4 * (ln >> 4) + r, n = n0 + (ln & 15);
-      if (m < a.M && n < a.N) {
-        if (YT) ((_Float16*)a.y)[(size_t)m * a.N + n] = (_Float16)s;
-        else ((float*)a.y)[(size_t)m * a.N + n] = s;
-      }
+      if (m < a.M && n < a.N) cq_store<YT>(a.y, a.epi, s, (size_t)m * a.N + n, n);
     }
   } else {
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const int m = m0 + 4 * g + r, n = n0 + j;
-      if (m < a.M && n < a.N) {
-        if (YT) ((_Float16*)a.y)[(size_t)m * a.N + n] = (_Float16)acc[r];
-        else ((float*)a.y)[(size_t)m * a.N + n] = acc[r];
-      }
+      if (m < a.M && n < a.N) cq_store<YT>(a.y, a.epi, acc[r], (size_t)m * a.N + n, n);
     }
   }
 }

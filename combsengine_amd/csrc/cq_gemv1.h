@@ -47,6 +47,7 @@ struct Gv1Args {
   int N, K, units;
   int rows;             // rows per wave task (R)
   int tasks;            // ceil(N / R)
+  CqEpi epi;
 };
 
 __shared__ __attribute__((aligned(16))) int8_t gv_xh[GV1_XMAX / 256 * GV1_XSTRIDE];
@@ -375,19 +376,13 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
     if ((a.units & (a.units - 1)) == 0) {
       // a row's lanes form an aligned group of `units` lanes: butterfly within it
       for (int o = a.units >> 1; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
-      if (myunit == 0 && myrow < nrows) {
-        if (YT) ((_Float16*)a.y)[r0 + myrow] = (_Float16)part;
-        else ((float*)a.y)[r0 + myrow] = part;
-      }
+      if (myunit == 0 && myrow < nrows) cq_store<YT>(a.y, a.epi, part, r0 + myrow, r0 + myrow);
     } else {
       for (int q = 0; q < a.rows; q++) {
         float v = myrow == q ? part : 0.0f;
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-        if (lane == 0 && q < nrows) {
-          if (YT) ((_Float16*)a.y)[r0 + q] = (_Float16)v;
-          else ((float*)a.y)[r0 + q] = v;
-        }
+        if (lane == 0 && q < nrows) cq_store<YT>(a.y, a.epi, v, r0 + q, r0 + q);
       }
     }
   };

@@ -16,6 +16,7 @@
 #include <string>
 
 #include "../../include/combs_qlinear.h"
+#include "cq_epi.h"
 
 #ifndef CQ_HSACO_PATH
 #error "CQ_HSACO_PATH must name the gfx950 code object to embed"
@@ -106,6 +107,7 @@ struct GemvArgs {
   int units;
   int kc;
   int lds_stride;
+  CqEpi epi;
 };
 struct GemmArgs {
   const void* w;
@@ -114,6 +116,7 @@ struct GemmArgs {
   long long row_bytes;
   int M, N, K;
   int units;
+  CqEpi epi;
 };
 struct LtArgs {
   const void* w;
@@ -123,6 +126,7 @@ struct LtArgs {
   float* part;
   long long row_bytes;
   int M, N, K, units, usplit;
+  CqEpi epi;
 };
 struct Gv1Args {
   const void* w;
@@ -130,6 +134,7 @@ struct Gv1Args {
   void* y;
   long long row_bytes;
   int N, K, units, rows, tasks;
+  CqEpi epi;
 };
 struct DequantArgs {
   const void* w;
@@ -355,7 +360,7 @@ static int gemv_waves(int units) {
 }
 
 static cq_status launch_gemv(DeviceModule* dm, const cq_weight* w, const void* x, int xt, int64_t m, void* y,
-                             int yt, hipStream_t s) {
+                             int yt, hipStream_t s, const CqEpi& epi) {
   const int fi = fmt_index(w->format);
   const int qk = block_values(w->format);
   const int64_t blocks = w->k / qk;
@@ -369,6 +374,7 @@ static cq_status launch_gemv(DeviceModule* dm, const cq_weight* w, const void* x
   a.N = (int)w->n;
   a.K = (int)w->k;
   a.units = (int)(qk == 256 ? blocks : (blocks + 3) / 4);
+  a.epi = epi;
   const int mrows = m < 16 ? (int)m : 16;
   const int xmul = xt ? 2 : 1;
   int kc = kGemvLdsBudget / (2 * xmul * mrows) - 8;
@@ -398,7 +404,8 @@ static int gemv1_waves(int format) { return format == CQ_Q4_K || format == CQ_Q5
 static bool gemv1_fits(const cq_weight* w) {
   return w->k % 256 == 0 && w->k <= kGv1MaxK && w->k / 256 <= 64;
 }
-static cq_status launch_gemv1(DeviceModule* dm, const cq_weight* w, const void* x, void* y, int yt, hipStream_t s) {
+static cq_status launch_gemv1(DeviceModule* dm, const cq_weight* w, const void* x, void* y, int yt, hipStream_t s,
+                              const CqEpi& epi) {
   const int fi = fmt_index(w->format);
   Gv1Args a;
   a.w = w->dev;
@@ -410,6 +417,7 @@ static cq_status launch_gemv1(DeviceModule* dm, const cq_weight* w, const void* 
   a.units = (int)(w->k / 256);
   a.rows = a.units >= 64 ? 1 : 64 / a.units;
   a.tasks = (int)((w->n + a.rows - 1) / a.rows);
+  a.epi = epi;
   const int nw = gemv1_waves(w->format);
   const int wgs = (a.tasks + nw - 1) / nw;
   int cap = env_int("COMBS_GEMV1_GRID", dm->cus);
@@ -426,7 +434,7 @@ static cq_status launch_gemv1(DeviceModule* dm, const cq_weight* w, const void* 
 // uses.  MT = 16 once m exceeds one 128-row block; NT = 2 when that still
 // gives every compute unit a workgroup.  COMBS_GEMM2_NT / COMBS_GEMM2_MT force them.
 static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* x, int64_t m, void* y, int yt,
-                              hipStream_t s) {
+                              hipStream_t s, const CqEpi& epi) {
   const int fi = fmt_index(w->format);
   LtArgs a;
   a.w = w->dev;
@@ -440,6 +448,7 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
   a.units = (int)(w->k / 256);
   a.part = nullptr;
   a.usplit = a.units;
+  a.epi = epi;
   int mt = env_int("COMBS_GEMM2_MT", 0);
   if (mt != 8 && mt != 16) mt = m > 128 ? 16 : 8;
   const long long mblk = (m + 16 * mt - 1) / (16 * mt);
@@ -483,7 +492,9 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
                               256, 1, 1, 0, s, params, nullptr);
     if (e != hipSuccess || !part_bytes) return e;
     long long mn = m * w->n;
-    void* rp[] = {&a.part, &y, &splits, &mn};
+    int n = (int)w->n;
+    CqEpi ep = epi;
+    void* rp[] = {&a.part, &y, &splits, &mn, &n, &ep};
     return hipModuleLaunchKernel(dm->reduce[yt], (unsigned)((mn + 255) / 256), 1, 1, 256, 1, 1, 0, s, rp, nullptr);
   };
   const hipError_t e = launch_all();
@@ -495,7 +506,7 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
 // Prefill GEMM (cq_gemm_*, K-quants): workgroups of nw waves x 16 weight rows
 // and 64 (fp16 x) or 32 (fp32 x) activation rows.
 static cq_status launch_gemm(DeviceModule* dm, const cq_weight* w, const void* x, int xt, int64_t m, void* y, int yt,
-                             hipStream_t s) {
+                             hipStream_t s, const CqEpi& epi) {
   const int fi = fmt_index(w->format);
   GemmArgs a;
   a.w = w->dev;
@@ -506,7 +517,8 @@ static cq_status launch_gemm(DeviceModule* dm, const cq_weight* w, const void* x
   a.N = (int)w->n;
   a.K = (int)w->k;
   a.units = (int)(w->k / 256);
-  if (!xt && env_int("COMBS_GEMM_KERNEL", 2) == 2) return launch_gemm2(dm, w, x, m, y, yt, s);
+  a.epi = epi;
+  if (!xt && env_int("COMBS_GEMM_KERNEL", 2) == 2) return launch_gemm2(dm, w, x, m, y, yt, s, epi);
   int nw = env_int("COMBS_GEMM_WAVES", 4);
   if (nw < 4 || nw > 8) nw = 4;  // the activation staging assumes >= 256 threads
   const int mb = xt ? 32 : 64;
@@ -518,8 +530,9 @@ static cq_status launch_gemm(DeviceModule* dm, const cq_weight* w, const void* x
   return CQ_OK;
 }
 
-cq_status cq_matmul_path(const cq_weight* w, const void* x, int x_dtype, int64_t m, void* y, int y_dtype, int path,
-                         void* stream) {
+// Shared by cq_matmul_path, cq_matmul_bias and cq_matmul_gate_up.
+static cq_status matmul_impl(const cq_weight* w, const void* x, int x_dtype, int64_t m, void* y, int y_dtype, int path,
+                             void* stream, const CqEpi& epi) {
   if (!w || !x || !y) return fail(CQ_ERR_NULL, "NULL weight, x or y");
   if (x_dtype != CQ_F16 && x_dtype != CQ_F32) return fail(CQ_ERR_BAD_DTYPE, "x_dtype %d", x_dtype);
   if (y_dtype != CQ_F16 && y_dtype != CQ_F32) return fail(CQ_ERR_BAD_DTYPE, "y_dtype %d", y_dtype);
@@ -536,10 +549,46 @@ cq_status cq_matmul_path(const cq_weight* w, const void* x, int x_dtype, int64_t
   // kernel.
   const bool kq = block_values(w->format) == 256;
   if (kq && (path == CQ_PATH_GEMM || (path == CQ_PATH_AUTO && m > 16)))
-    return launch_gemm(dm, w, x, xt, m, y, yt, (hipStream_t)stream);
+    return launch_gemm(dm, w, x, xt, m, y, yt, (hipStream_t)stream, epi);
   if (m == 1 && !xt && path != CQ_PATH_GEMV && gemv1_fits(w) && env_int("COMBS_GEMV1", 1))
-    return launch_gemv1(dm, w, x, y, yt, (hipStream_t)stream);
-  return launch_gemv(dm, w, x, xt, m, y, yt, (hipStream_t)stream);
+    return launch_gemv1(dm, w, x, y, yt, (hipStream_t)stream, epi);
+  return launch_gemv(dm, w, x, xt, m, y, yt, (hipStream_t)stream, epi);
+}
+
+cq_status cq_matmul_path(const cq_weight* w, const void* x, int x_dtype, int64_t m, void* y, int y_dtype, int path,
+                         void* stream) {
+  const CqEpi none{};
+  return matmul_impl(w, x, x_dtype, m, y, y_dtype, path, stream, none);
+}
+
+cq_status cq_matmul_bias(const cq_weight* w, const void* x, int x_dtype, int64_t m, const void* bias, int bias_dtype,
+                         void* y, int y_dtype, void* stream) {
+  if (bias_dtype != CQ_F16 && bias_dtype != CQ_F32) return fail(CQ_ERR_BAD_DTYPE, "bias_dtype %d", bias_dtype);
+  CqEpi epi{};
+  epi.bias = bias;
+  epi.bias_f16 = bias_dtype == CQ_F16;
+  return matmul_impl(w, x, x_dtype, m, y, y_dtype, CQ_PATH_AUTO, stream, epi);
+}
+
+// up(x) is written to y first (in y's dtype, as the reference's f16 model
+// rounds each projection's output), then gate(x)'s epilogue reads it back
+// from y and overwrites it with act(gate) * up: no scratch memory.
+cq_status cq_matmul_gate_up(const cq_weight* gate, const cq_weight* up, const void* x, int x_dtype, int64_t m,
+                            int act, void* y, int y_dtype, void* stream) {
+  if (!gate || !up) return fail(CQ_ERR_NULL, "NULL gate or up weight");
+  if (gate->n != up->n || gate->k != up->k)
+    return fail(CQ_ERR_BAD_SHAPE, "gate [%lld, %lld] and up [%lld, %lld] differ", (long long)gate->n,
+                (long long)gate->k, (long long)up->n, (long long)up->k);
+  if (act != CQ_ACT_SILU && act != CQ_ACT_GELU_TANH && act != CQ_ACT_GELU)
+    return fail(CQ_ERR_BAD_SHAPE, "unknown activation %d", act);
+  const CqEpi none{};
+  cq_status st = matmul_impl(up, x, x_dtype, m, y, y_dtype, CQ_PATH_AUTO, stream, none);
+  if (st != CQ_OK) return st;
+  CqEpi epi{};
+  epi.aux = y;
+  epi.aux_f16 = y_dtype == CQ_F16;
+  epi.act = act;
+  return matmul_impl(gate, x, x_dtype, m, y, y_dtype, CQ_PATH_AUTO, stream, epi);
 }
 
 cq_status cq_matmul(const cq_weight* w, const void* x, int x_dtype, int64_t m, void* y, int y_dtype, void* stream) {

@@ -89,12 +89,12 @@ GEMM2_KERNEL(cq_gemm2_q6_k_n2_m8_yf16, CQ_Q6_K, 1, 2, 8)
 GEMM2_KERNEL(cq_gemm2_q6_k_n2_m16_yf32, CQ_Q6_K, 0, 2, 16)
 GEMM2_KERNEL(cq_gemm2_q6_k_n2_m16_yf16, CQ_Q6_K, 1, 2, 16)
 extern "C" __global__ void __launch_bounds__(256) cq_splitk_reduce_yf32(const float* part, void* y, int splits,
-                                                                       long long mn) {
-  splitk_reduce_body<0>(part, y, splits, mn);
+                                                                       long long mn, int n, CqEpi epi) {
+  splitk_reduce_body<0>(part, y, splits, mn, n, epi);
 }
 extern "C" __global__ void __launch_bounds__(256) cq_splitk_reduce_yf16(const float* part, void* y, int splits,
-                                                                       long long mn) {
-  splitk_reduce_body<1>(part, y, splits, mn);
+                                                                       long long mn, int n, CqEpi epi) {
+  splitk_reduce_body<1>(part, y, splits, mn, n, epi);
 }
 extern "C" __global__ void __launch_bounds__(256) cq_xsums_f16(const _Float16* x, _Float16* xs, int M, int K) {
   xsums_body(x, xs, M, K);

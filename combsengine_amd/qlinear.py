@@ -162,9 +162,8 @@ class QuantWeight:
         return self._h
 
     # -- compute ---------------------------------------------------------------
-    def matmul_into(self, x, y, path: int = L.CQ_PATH_AUTO, stream=None):
-        """Launch y[m, n] = x[m, k] . W^T on the current (or given) stream.
-        x: CUDA fp16/fp32 contiguous [m, k]; y: CUDA fp32/fp16 contiguous [m, n]."""
+    def _io(self, x, y):
+        """Validates x [m, k] / y [m, n_out] device tensors; returns (m, xt, yt)."""
         if not (x.is_cuda and y.is_cuda) or x.device != y.device:
             raise ModelError("x and y must be device tensors on the weight's device")
         if x.dim() != 2 or x.shape[1] != self._k or not x.is_contiguous():
@@ -176,9 +175,33 @@ class QuantWeight:
         yt = _XT.get(str(y.dtype))
         if xt is None or yt is None:
             raise ModelError(f"unsupported dtypes x={x.dtype} y={y.dtype}")
+        return m, xt, yt
+
+    def matmul_into(self, x, y, path: int = L.CQ_PATH_AUTO, stream=None):
+        """Launch y[m, n] = x[m, k] . W^T on the current (or given) stream.
+        x: CUDA fp16/fp32 contiguous [m, k]; y: CUDA fp32/fp16 contiguous [m, n]."""
+        m, xt, yt = self._io(x, y)
         s = stream if stream is not None else _stream_ptr(x.device)
         st = L.lib().cq_matmul_path(self._h, x.data_ptr(), xt, m, y.data_ptr(), yt, path, s)
         _check(st, "cq_matmul", f"{self.format.name.lower()} matmul input", [m, self._k], list(x.shape))
+        return y
+
+    def matmul_bias_into(self, x, bias, y, stream=None):
+        """y = x . W^T + bias[n] with the bias add in the kernels' epilogue
+        (Linear::forward's quantized branch, qlinear.rs:84-98).  bias: device
+        fp32/fp16 [n_out], or None."""
+        m, xt, yt = self._io(x, y)
+        bp, bt = 0, L.CQ_F32
+        if bias is not None:
+            if not bias.is_cuda or bias.device != x.device or bias.numel() != self._n_out or not bias.is_contiguous():
+                raise BadShape(f"{self.format.name.lower()} bias", [self._n_out], list(bias.shape))
+            bt = _XT.get(str(bias.dtype))
+            if bt is None:
+                raise ModelError(f"unsupported bias dtype {bias.dtype}")
+            bp = bias.data_ptr()
+        s = stream if stream is not None else _stream_ptr(x.device)
+        st = L.lib().cq_matmul_bias(self._h, x.data_ptr(), xt, m, bp, bt, y.data_ptr(), yt, s)
+        _check(st, "cq_matmul_bias", f"{self.format.name.lower()} matmul input", [m, self._k], list(x.shape))
         return y
 
     def matmul_device(self, x, m: Optional[int] = None, out_dtype=None, path: int = L.CQ_PATH_AUTO):
@@ -216,11 +239,45 @@ class QuantLinearOp:
         y = self.w.matmul_device(x.reshape(b * s, k), out_dtype=x.dtype)
         return y.reshape(b, s, self.w.n_out())
 
+    def forward_bias(self, x, bias):
+        """forward(x) + bias broadcast over rows, one kernel (qlinear.rs:84-98)."""
+        b, s, k = x.shape
+        y = _torch().empty((b * s, self.w.n_out()), dtype=x.dtype, device=x.device)
+        self.w.matmul_bias_into(x.reshape(b * s, k).contiguous(), bias.contiguous(), y)
+        return y.reshape(b, s, self.w.n_out())
+
     def dims(self):
         return [self.w.n_out(), self.w.k()]
 
     def vram_bytes(self) -> int:
         return self.w.vram_bytes()
+
+
+class Activation(enum.IntEnum):
+    """combs_formats::Activation as applied by act.rs:20-30."""
+    Silu = L.CQ_ACT_SILU
+    GeluTanh = L.CQ_ACT_GELU_TANH
+    Gelu = L.CQ_ACT_GELU
+
+
+def gated_up(activation, gate: "QuantLinearOp", up: "QuantLinearOp", h):
+    """`act::apply(activation, gate.forward(h)) * up.forward(h)`
+    (llama.rs:301-303) as one library call: up's product goes to the output,
+    gate's kernel epilogue applies the activation and the product in place.
+    h [batch, seq, k] fp16/fp32 -> [batch, seq, n] in h's dtype."""
+    torch = _torch()
+    b, s, k = h.shape
+    if gate.dims() != up.dims() or gate.dims()[1] != k:
+        raise BadShape("gate/up", gate.dims(), up.dims())
+    n = gate.dims()[0]
+    x = h.reshape(b * s, k).contiguous()
+    y = torch.empty((b * s, n), dtype=h.dtype, device=h.device)
+    gate.w._io(x, y)
+    xt, yt = _XT[str(x.dtype)], _XT[str(y.dtype)]
+    st = L.lib().cq_matmul_gate_up(gate.w.handle, up.w.handle, x.data_ptr(), xt, b * s, int(Activation(activation)),
+                                   y.data_ptr(), yt, _stream_ptr(x.device))
+    _check(st, "cq_matmul_gate_up", "gate/up input", [b * s, k], list(x.shape))
+    return y.reshape(b, s, n)
 
 
 class Linear:
@@ -247,11 +304,11 @@ class Linear:
         if self.dense is not None:
             # fp32 accumulation, output in the activation dtype
             out = (x.float() @ self.dense.t().float()).to(x.dtype)
-        else:
-            out = self.quant.forward(x)
-        if bias is not None:
-            out = out + bias.to(out.dtype).reshape(1, 1, -1)
-        return out
+            if bias is not None:
+                out = out + bias.to(out.dtype).reshape(1, 1, -1)
+            return out
+        # quantized: the bias add runs in the kernels' epilogue
+        return self.quant.forward(x) if bias is None else self.quant.forward_bias(x, bias)
 
 
 def try_quant_linear(source, name: str, device=None) -> Optional[QuantLinearOp]:

@@ -109,6 +109,27 @@ typedef enum { CQ_PATH_AUTO = 0, CQ_PATH_GEMV = 1, CQ_PATH_GEMM = 2 } cq_path;
 cq_status cq_matmul_path(const cq_weight* w, const void* x, int x_dtype, int64_t m, void* y, int y_dtype,
                          int path, void* stream);
 
+/* cq_matmul with the bias add fused into the kernels' epilogue:
+ * y[m,n] = x[m,k] . dequant(W)^T + bias[n], one rounding to y_dtype.
+ * Replaces the quantized branch of Linear::forward, op.forward(x) followed
+ * by `out + b` broadcast over rows (qlinear.rs:84-98).  bias: device [n],
+ * bias_dtype CQ_F32 or CQ_F16; NULL means no bias (the reference's None). */
+cq_status cq_matmul_bias(const cq_weight* w, const void* x, int x_dtype, int64_t m, const void* bias,
+                         int bias_dtype, void* y, int y_dtype, void* stream);
+
+/* Activations of the gated MLP (combs_formats::Activation, applied by
+ * act.rs:20-30): SiLU x*sigmoid(x); tanh-approximated GELU; exact (erf) GELU. */
+typedef enum { CQ_ACT_SILU = 0, CQ_ACT_GELU_TANH = 1, CQ_ACT_GELU = 2 } cq_act;
+
+/* Gated MLP input projection: y[m,n] = act(x . gate^T) * (x . up^T).
+ * Replaces `act::apply(activation, gate.forward(h)) * up.forward(h)`
+ * (llama.rs:301-303).  gate and up have the same [n, k] (formats may
+ * differ).  up's product is written to y first, in y_dtype, and gate's
+ * kernel epilogue reads it back and overwrites it: no scratch memory, two
+ * launches on `stream`, one read of x per projection. */
+cq_status cq_matmul_gate_up(const cq_weight* gate, const cq_weight* up, const void* x, int x_dtype, int64_t m,
+                            int act, void* y, int y_dtype, void* stream);
+
 /* Bit-exact dequantisation of a device block stream to f32 (validation).
  * Replaces dequantize_*_gpu (qmatmul.rs:171-190, 530-573, 1232-1305); the
  * result equals gguf.rs dequantize_* (gguf.rs:755-999) bit for bit. */

@@ -125,6 +125,48 @@ def dense_gemm(x: np.ndarray, w: np.ndarray, threads: int = 1) -> np.ndarray:
     return out
 
 
+# ---- the steps either side of the op ---------------------------------------
+
+ACT_SILU, ACT_GELU_TANH, ACT_GELU = 0, 1, 2
+
+
+def activation(kind: int, v) -> np.ndarray:
+    """The gated MLP activations of combs-models act.rs:20-30, in float64:
+    SiLU = burn's silu, x * sigmoid(x); GeluTanh = gelu_tanh (act.rs:10-17),
+    x/2 * (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))); Gelu = burn's exact
+    gelu, x/2 * (1 + erf(x / sqrt(2))).  Pinned by act.rs:41-52's known
+    values (GeluTanh), silu(x) - silu(-x) = x and silu(0) = 0, and the
+    standard normal CDF, gelu(x) = x * Phi(x) (Phi(1) = 0.8413447460685429)."""
+    from scipy.special import erf
+    v = np.asarray(v, np.float64)
+    if kind == ACT_SILU:
+        return v / (1.0 + np.exp(-v))
+    if kind == ACT_GELU_TANH:
+        c = 0.7978845608028654  # sqrt(2/pi), act.rs:13
+        return 0.5 * v * (1.0 + np.tanh(c * (v + 0.044715 * v ** 3)))
+    if kind == ACT_GELU:
+        return 0.5 * v * (1.0 + erf(v / np.sqrt(2.0)))
+    raise ValueError(f"unknown activation {kind}")
+
+
+def linear(fmt: int, data, x: np.ndarray, n: int, k: int, bias=None) -> np.ndarray:
+    """Linear::forward's quantized branch (qlinear.rs:84-98): the op's
+    y = x . W^T (fused_matmul, the reference kernels' arithmetic) then
+    `out + b` broadcast over rows; float64 result."""
+    y = fused_matmul(fmt, data, x, n, k).astype(np.float64)
+    if bias is not None:
+        y = y + np.asarray(bias, np.float64).reshape(1, -1)
+    return y
+
+
+def gated_up(kind: int, gate, up, x: np.ndarray, n: int, k: int) -> np.ndarray:
+    """llama.rs:301-303: act(gate.forward(h)) * up.forward(h); gate and up
+    are (fmt, data) pairs of the same [n, k] shape; float64 result."""
+    g = fused_matmul(gate[0], gate[1], x, n, k).astype(np.float64)
+    u = fused_matmul(up[0], up[1], x, n, k).astype(np.float64)
+    return activation(kind, g) * u
+
+
 # ---- the reference's synthetic fixtures -----------------------------------
 
 def lcg_bytes(n: int, seed: int) -> bytes:

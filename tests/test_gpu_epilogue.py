@@ -1,0 +1,156 @@
+"""GPU parity of the fused output epilogues against the CPU oracle, through
+the C ABI: the bias add of Linear::forward (qlinear.rs:84-98) and the gated
+MLP product act(gate(h)) * up(h) (llama.rs:301-303, act.rs:20-30).
+
+Every kernel path is covered: the single-row GEMV (m = 1), the MFMA GEMV
+(m = 4), the prefill GEMM (m >= 64, with and without split K, whose reduction
+applies the epilogue) and the fp32-activation GEMM.  Expected values come
+from the oracle's fused matmul in float64; the bar is the matmul's own,
+|g - e| <= rel * max(|e|, 1)."""
+import numpy as np
+import pytest
+
+import oracle as O
+from combsengine_amd import Activation, Linear, QuantFormat, QuantLinearOp, QuantWeight, gated_up, quantize
+from combsengine_amd import _lib as L
+
+pytestmark = pytest.mark.gpu
+
+FMTS = [QuantFormat.Q4_0, QuantFormat.Q5_0, QuantFormat.Q8_0, QuantFormat.Q4K, QuantFormat.Q5K, QuantFormat.Q6K]
+KQ = [QuantFormat.Q4K, QuantFormat.Q5K, QuantFormat.Q6K]
+
+
+def _weight(fmt, n, k, seed):
+    rng = np.random.default_rng(seed)
+    data = quantize(fmt, rng.normal(0, 0.02, (n, k)).astype(np.float32))
+    return data, QuantWeight.from_gguf_bytes(fmt, data, n, k)
+
+
+def _x(m, k, seed):
+    return np.random.default_rng(seed).normal(0, 1, (m, k)).astype(np.float16).astype(np.float32)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("m", [1, 4, 64])
+@pytest.mark.parametrize("bias_dt", ["f32", "f16"])
+@pytest.mark.parametrize("y_dt", ["f32", "f16"])
+def test_bias_epilogue(cuda, fmt, m, bias_dt, y_dt):
+    import torch
+    n, k = 300, 2048
+    data, w = _weight(fmt, n, k, 10 + int(fmt))
+    x = _x(m, k, m)
+    b = np.random.default_rng(7).normal(0, 2, n).astype(np.float32)
+    bt = torch.float32 if bias_dt == "f32" else torch.float16
+    b = b.astype(np.float16).astype(np.float32) if bias_dt == "f16" else b
+    expect = O.linear(int(fmt), data, x, n, k, b)
+    print(f"bias {fmt.name} m={m} bias={bias_dt} y={y_dt}", flush=True)
+    yt = torch.float32 if y_dt == "f32" else torch.float16
+    y = torch.empty((m, n), dtype=yt, device="cuda")
+    w.matmul_bias_into(torch.from_numpy(x).cuda().half(), torch.from_numpy(b).cuda().to(bt), y)
+    O.assert_close(y.float().cpu().numpy(), expect, 1e-4 if fmt == QuantFormat.Q4_0 and y_dt == "f32" else 1e-3)
+
+
+@pytest.mark.parametrize("fmt", KQ)
+@pytest.mark.parametrize("split", ["1", "3"])
+def test_bias_epilogue_prefill_split_and_fp32_x(cuda, monkeypatch, fmt, split):
+    """The split-K reduction applies the bias; fp32 activations take the
+    fp32-x GEMM, whose epilogue is the same."""
+    import torch
+    monkeypatch.setenv("COMBS_GEMM2_SPLIT", split)
+    n, k, m = 200, 3072, 130
+    data, w = _weight(fmt, n, k, 20 + int(fmt))
+    x = _x(m, k, 3)
+    b = np.random.default_rng(8).normal(0, 1, n).astype(np.float32)
+    expect = O.linear(int(fmt), data, x, n, k, b)
+    print(f"bias prefill {fmt.name} split={split}", flush=True)
+    for xt in (torch.float16, torch.float32):
+        y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        w.matmul_bias_into(torch.from_numpy(x).cuda().to(xt), torch.from_numpy(b).cuda(), y)
+        O.assert_close(y.cpu().numpy(), expect, 1e-3, f"x {xt}")
+
+
+def test_bias_none_equals_matmul(cuda):
+    import torch
+    data, w = _weight(QuantFormat.Q4K, 100, 1024, 5)
+    x = torch.from_numpy(_x(3, 1024, 1)).cuda().half()
+    a = torch.empty((3, 100), device="cuda")
+    b = torch.empty((3, 100), device="cuda")
+    w.matmul_into(x, a)
+    w.matmul_bias_into(x, None, b)
+    assert torch.equal(a, b)
+
+
+PAIRS = [(QuantFormat.Q4K, QuantFormat.Q4K), (QuantFormat.Q4K, QuantFormat.Q6K), (QuantFormat.Q8_0, QuantFormat.Q5_0)]
+
+
+@pytest.mark.parametrize("gf,uf", PAIRS)
+@pytest.mark.parametrize("act", [Activation.Silu, Activation.GeluTanh, Activation.Gelu])
+@pytest.mark.parametrize("m", [1, 4, 64, 130])
+@pytest.mark.parametrize("y_dt", ["f32", "f16"])
+def test_gate_up_epilogue(cuda, gf, uf, act, m, y_dt):
+    """y = act(x.G^T) * (x.U^T).  With an fp16 output the library rounds up's
+    product to fp16 (as the reference's f16 model rounds every projection),
+    so the expected value does too; the bar then carries the two fp16
+    roundings (2^-11 relative each) on top of the matmul's 1e-3."""
+    import torch
+    n, k = 260, 2048
+    gd, gw = _weight(gf, n, k, 30 + int(gf))
+    ud, uw = _weight(uf, n, k, 40 + int(uf))
+    x = _x(m, k, 50 + m)
+    g = O.fused_matmul(int(gf), gd, x, n, k).astype(np.float64)
+    u = O.fused_matmul(int(uf), ud, x, n, k).astype(np.float64)
+    if y_dt == "f16":
+        u = u.astype(np.float16).astype(np.float64)
+    expect = O.activation(int(act), g) * u
+    print(f"gate_up {gf.name}/{uf.name} {act.name} m={m} y={y_dt}", flush=True)
+    h = torch.from_numpy(x).cuda().half().reshape(1, m, k)
+    if y_dt == "f32":
+        h = h.float()  # y follows h's dtype; fp32 h takes the fp32-x kernels
+    y = gated_up(act, QuantLinearOp(gw), QuantLinearOp(uw), h)
+    assert y.shape == (1, m, n) and y.dtype == h.dtype
+    O.assert_close(y.float().cpu().numpy(), expect, 1e-3 if y_dt == "f32" else 2e-3)
+
+
+@pytest.mark.parametrize("split", ["1", "4"])
+def test_gate_up_prefill_split(cuda, monkeypatch, split):
+    import torch
+    monkeypatch.setenv("COMBS_GEMM2_SPLIT", split)
+    n, k, m = 300, 4096, 200
+    gd, gw = _weight(QuantFormat.Q4K, n, k, 61)
+    ud, uw = _weight(QuantFormat.Q4K, n, k, 62)
+    x = _x(m, k, 63)
+    expect = O.gated_up(O.ACT_SILU, (int(QuantFormat.Q4K), gd), (int(QuantFormat.Q4K), ud), x, n, k)
+    print(f"gate_up prefill split={split}", flush=True)
+    y = torch.empty((m, n), device="cuda")
+    st = L.lib().cq_matmul_gate_up(gw.handle, uw.handle, torch.from_numpy(x).cuda().half().data_ptr(), L.CQ_F16, m,
+                                   L.CQ_ACT_SILU, y.data_ptr(), L.CQ_F32, 0)
+    assert st == L.CQ_OK, L.last_error()
+    torch.cuda.synchronize()
+    O.assert_close(y.cpu().numpy(), expect, 1e-3)
+
+
+def test_linear_forward_bias_fused(cuda):
+    """Linear::forward with a bias (qlinear.rs:84-98) on the quantized branch
+    takes the fused epilogue and matches the dense branch's definition."""
+    import torch
+    n, k = 128, 1024
+    data, w = _weight(QuantFormat.Q6K, n, k, 70)
+    x = _x(6, k, 71)
+    b = np.random.default_rng(72).normal(0, 1, n).astype(np.float32)
+    lin = Linear.Quant(QuantLinearOp(w))
+    out = lin.forward(torch.from_numpy(x).cuda().float().reshape(2, 3, k), torch.from_numpy(b).cuda())
+    assert out.shape == (2, 3, n)
+    O.assert_close(out.cpu().numpy().reshape(6, n), O.linear(int(QuantFormat.Q6K), data, x, n, k, b), 1e-3)
+
+
+def test_gate_up_rejects_mismatched_shapes(cuda):
+    import torch
+    _, a = _weight(QuantFormat.Q4K, 64, 512, 1)
+    _, b = _weight(QuantFormat.Q4K, 32, 512, 2)
+    x = torch.zeros((1, 512), dtype=torch.float16, device="cuda")
+    y = torch.zeros((1, 64), device="cuda")
+    st = L.lib().cq_matmul_gate_up(a.handle, b.handle, x.data_ptr(), L.CQ_F16, 1, L.CQ_ACT_SILU, y.data_ptr(),
+                                   L.CQ_F32, 0)
+    assert st == L.CQ_ERR_BAD_SHAPE and "differ" in L.last_error()
+    st = L.lib().cq_matmul_gate_up(a.handle, a.handle, x.data_ptr(), L.CQ_F16, 1, 7, y.data_ptr(), L.CQ_F32, 0)
+    assert st == L.CQ_ERR_BAD_SHAPE

@@ -228,3 +228,41 @@ def test_dense_gemm_matches_ref():
     w = rng.normal(size=(40, 576)).astype(np.float32)
     O.assert_close(O.dense_gemm(x, w, 1), O.ref_matmul(x, w), 1e-4)
     O.assert_close(O.dense_gemm(x, w, 4), O.ref_matmul(x, w), 1e-4)
+
+
+def test_activation_gelu_tanh_known_values():
+    # act.rs:41-52: torch gelu(approximate="tanh") at -1, 0, 1, 2
+    got = O.activation(O.ACT_GELU_TANH, [-1.0, 0.0, 1.0, 2.0])
+    assert np.all(np.abs(got - [-0.158808, 0.0, 0.841192, 1.954597]) < 1e-5)
+
+
+def test_activation_silu_identities():
+    v = np.linspace(-30, 30, 1201)
+    s = O.activation(O.ACT_SILU, v)
+    assert O.activation(O.ACT_SILU, [0.0])[0] == 0.0
+    # x*sigmoid(x) - (-x)*sigmoid(-x) = x (sigmoid(x) + sigmoid(-x) = 1)
+    assert np.allclose(s - O.activation(O.ACT_SILU, -v), v, rtol=0, atol=1e-12)
+    # sigmoid(x) -> 1 and -> 0 at the ends; sigmoid(1) = e / (1 + e)
+    assert abs(s[-1] - 30.0) < 1e-11 and abs(s[0]) < 1e-11
+    assert abs(O.activation(O.ACT_SILU, [1.0])[0] - np.e / (1 + np.e)) < 1e-15
+
+
+def test_activation_gelu_is_x_times_normal_cdf():
+    # Phi(1) = 0.8413447460685429, Phi(2) = 0.9772498680518208 (normal tables)
+    got = O.activation(O.ACT_GELU, [1.0, -1.0, 2.0, 0.0])
+    want = [0.8413447460685429, -(1 - 0.8413447460685429), 2 * 0.9772498680518208, 0.0]
+    assert np.allclose(got, want, rtol=0, atol=1e-15)
+    # tanh form approximates the exact one to < 1e-3 on [-4, 4]
+    v = np.linspace(-4, 4, 801)
+    assert np.max(np.abs(O.activation(O.ACT_GELU, v) - O.activation(O.ACT_GELU_TANH, v))) < 1e-3
+
+
+def test_linear_bias_and_gated_up_compose_the_op():
+    k, n, m = 256, 5, 2
+    data = O.synth_q4_k(n)
+    x = O.x_pattern(m, k).reshape(m, k)
+    y = O.fused_matmul(O.Q4_K, data, x, n, k).astype(np.float64)
+    b = np.arange(n) - 2.0
+    assert np.array_equal(O.linear(O.Q4_K, data, x, n, k, b), y + b)
+    g = O.gated_up(O.ACT_SILU, (O.Q4_K, data), (O.Q4_K, data), x, n, k)
+    assert np.allclose(g, y * y / (1 + np.exp(-y)), rtol=1e-15, atol=0)

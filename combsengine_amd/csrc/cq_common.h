@@ -17,7 +17,9 @@ typedef uint32_t u4v __attribute__((ext_vector_type(4)));
 typedef uint32_t u2v __attribute__((ext_vector_type(2)));
 
 // GGML type ids, as in the GGUF file format.
-enum : int { CQ_Q4_0 = 2, CQ_Q5_0 = 6, CQ_Q8_0 = 8, CQ_Q4_K = 12, CQ_Q5_K = 13, CQ_Q6_K = 14 };
+enum : int {
+  CQ_Q4_0 = 2, CQ_Q4_1 = 3, CQ_Q5_0 = 6, CQ_Q5_1 = 7, CQ_Q8_0 = 8, CQ_Q4_K = 12, CQ_Q5_K = 13, CQ_Q6_K = 14
+};
 
 __device__ __forceinline__ uint32_t ld_u16(const uint8_t* p) {
   uint16_t v;

@@ -37,6 +37,25 @@ __device__ __forceinline__ void dequant_chunk(const uint8_t* __restrict__ w, flo
       v[j] = (float)lo * d;
       v[j + 16] = (float)hi * d;
     }
+  } else if constexpr (FMT == CQ_Q4_1) {  // gguf.rs:798-820: q * d + m
+    const uint8_t* b = w + c * 20;
+    const float d = f16_bits_to_f32(ld_u16(b)), m = f16_bits_to_f32(ld_u16(b + 2));
+    for (int j = 0; j < 16; j++) {
+      const uint32_t byte = b[4 + j];
+      v[j] = (float)(byte & 0x0F) * d + m;
+      v[j + 16] = (float)(byte >> 4) * d + m;
+    }
+  } else if constexpr (FMT == CQ_Q5_1) {  // gguf.rs:851-874: 5-bit q * d + m
+    const uint8_t* b = w + c * 24;
+    const float d = f16_bits_to_f32(ld_u16(b)), m = f16_bits_to_f32(ld_u16(b + 2));
+    const uint32_t qh = ld_u32(b + 4);
+    for (int j = 0; j < 16; j++) {
+      const uint32_t byte = b[8 + j];
+      const uint32_t lo = (byte & 0x0F) | (((qh >> j) & 1u) << 4);
+      const uint32_t hi = (byte >> 4) | (((qh >> (j + 16)) & 1u) << 4);
+      v[j] = (float)lo * d + m;
+      v[j + 16] = (float)hi * d + m;
+    }
   } else if constexpr (FMT == CQ_Q8_0) {  // gguf.rs:779-794
     const uint8_t* b = w + c * 34;
     const float d = f16_bits_to_f32(ld_u16(b));

@@ -364,6 +364,81 @@ __device__ __forceinline__ void compute_q50(const FragQ50& f, const XRow<XT>& xr
   }
 }
 
+// Q4_1 / Q5_1: the asymmetric twins of Q4_0 / Q5_0, value = q * d + m with
+// an fp16 min m per block (gguf.rs:798-820, 851-874): 20-byte block
+// [d][m][qs 16], 24-byte block [d][m][qh u32][qs 16].  B = q (0..15 / 0..31,
+// exact in fp16); the m term is m * sum(x of the block), the sum taken by one
+// more MFMA against B = 1.  The reference serves these formats through its
+// dense path only (dequantise, then f32 matmul).
+struct FragQ41 {
+  uint32_t q[LB], dm[LB];
+};
+__device__ __forceinline__ void load_q41(FragQ41& f, const uint8_t* b, int g, int nb) {
+#pragma unroll
+  for (int i = 0; i < LB; i++) {
+    const int ii = i < nb ? i : 0;
+    f.dm[i] = ld_u32(b + 20 * ii);
+    f.q[i] = ld_u32(b + 20 * ii + 4 + 4 * g);
+  }
+}
+struct FragQ51 {
+  uint32_t q[LB], h[LB], dm[LB];
+};
+__device__ __forceinline__ void load_q51(FragQ51& f, const uint8_t* b, int g, int nb) {
+#pragma unroll
+  for (int i = 0; i < LB; i++) {
+    const int ii = i < nb ? i : 0;
+    f.dm[i] = ld_u32(b + 24 * ii);
+    f.h[i] = ld_u32(b + 24 * ii + 4);
+    f.q[i] = ld_u32(b + 24 * ii + 8 + 4 * g);
+  }
+}
+// acc += d * (x . q) + m * sum(x) for one block.
+template <int XT>
+__device__ __forceinline__ void affine_block(const A8<XT>& a, const h8& b, uint32_t dm, f4& acc) {
+  const uint32_t one = 0x3C003C00u;  // fp16 1.0 pair
+  const h8 ones = mk_h8(one, one, one, one);
+  const f4 c = mfma_x<XT>(a, b, f4{0, 0, 0, 0});
+  const f4 s = mfma_x<XT>(a, ones, f4{0, 0, 0, 0});
+  const float d = f16_bits_to_f32(dm & 0xFFFFu), m = f16_bits_to_f32(dm >> 16);
+#pragma unroll
+  for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(d, c[r], __builtin_fmaf(m, s[r], acc[r]));
+}
+template <int XT>
+__device__ __forceinline__ void compute_q41(const FragQ41& f, const XRow<XT>& xr, int k0, int g, int nb, f4& acc) {
+  const h2 one = hsplat(1.0f), c_lo = hsplat(-1024.0f);
+  const h2 s16 = hsplat(0.0625f), c_hi = hsplat(-64.0f);
+#pragma unroll
+  for (int i = 0; i < LB; i++) {
+    if (i >= nb) break;
+    const uint32_t p1 = perm(C64, f.q[i], SEL_B0_E_B1_E), p2 = perm(C64, f.q[i], SEL_B2_E_B3_E);
+    const h8 b = mk_h8(pk_fma(p1 & 0x640F640Fu, one, c_lo), pk_fma(p2 & 0x640F640Fu, one, c_lo),
+                       pk_fma(p1 & 0x64F064F0u, s16, c_hi), pk_fma(p2 & 0x64F064F0u, s16, c_hi));
+    const int kb = k0 + 32 * i;
+    affine_block<XT>(load_a4x2<XT>(xr, kb + 4 * g, kb + 16 + 4 * g), b, f.dm[i], acc);
+  }
+}
+template <int XT>
+__device__ __forceinline__ void compute_q51(const FragQ51& f, const XRow<XT>& xr, int k0, int g, int nb, f4& acc) {
+  const h2 one = hsplat(1.0f), c_lo = hsplat(-1024.0f);
+  const h2 s16 = hsplat(0.0625f), c_hi = hsplat(-64.0f);
+#pragma unroll
+  for (int i = 0; i < LB; i++) {
+    if (i >= nb) break;
+    const uint32_t q = f.q[i];
+    const uint32_t hl = spread4(f.h[i] >> (4 * g));
+    const uint32_t hh = spread4(f.h[i] >> (16 + 4 * g));
+    const uint32_t z = bfi(0x10101010u, hl << 4, q);
+    const uint32_t hx = hh | C64;
+    const h8 b = mk_h8(pk_fma(perm(C64, z, SEL_B0_E_B1_E) & 0x641F641Fu, one, c_lo),
+                       pk_fma(perm(C64, z, SEL_B2_E_B3_E) & 0x641F641Fu, one, c_lo),
+                       pk_fma(perm(hx, q, SEL_X_B01) & 0x65F065F0u, s16, c_hi),
+                       pk_fma(perm(hx, q, SEL_X_B23) & 0x65F065F0u, s16, c_hi));
+    const int kb = k0 + 32 * i;
+    affine_block<XT>(load_a4x2<XT>(xr, kb + 4 * g, kb + 16 + 4 * g), b, f.dm[i], acc);
+  }
+}
+
 // Q8_0: 34-byte block [d][qs 32 x i8] (gguf.rs:779-794).  Lane group g takes
 // qs[8g, 8g+8) = k 8g..8g+7.  i8 s -> fp16 via (s ^ 0x80) = s + 128 placed
 // under a 0x64 high byte: 1024 + s + 128, minus 1152.
@@ -405,6 +480,8 @@ template <> struct FmtTraits<CQ_Q5_K> { static constexpr int vals = 256, bytes =
 template <> struct FmtTraits<CQ_Q6_K> { static constexpr int vals = 256, bytes = 210; typedef FragQ6K Frag; };
 template <> struct FmtTraits<CQ_Q4_0> { static constexpr int vals = 32 * LB, bytes = 18 * LB; typedef FragQ40 Frag; };
 template <> struct FmtTraits<CQ_Q5_0> { static constexpr int vals = 32 * LB, bytes = 22 * LB; typedef FragQ50 Frag; };
+template <> struct FmtTraits<CQ_Q4_1> { static constexpr int vals = 32 * LB, bytes = 20 * LB; typedef FragQ41 Frag; };
+template <> struct FmtTraits<CQ_Q5_1> { static constexpr int vals = 32 * LB, bytes = 24 * LB; typedef FragQ51 Frag; };
 template <> struct FmtTraits<CQ_Q8_0> { static constexpr int vals = 32 * LB, bytes = 34 * LB; typedef FragQ80 Frag; };
 
 template <int FMT>
@@ -414,6 +491,8 @@ __device__ __forceinline__ void load_unit(typename FmtTraits<FMT>::Frag& f, cons
   else if constexpr (FMT == CQ_Q6_K) load_q6k(f, p, g);
   else if constexpr (FMT == CQ_Q4_0) load_q40(f, p, g, nb);
   else if constexpr (FMT == CQ_Q5_0) load_q50(f, p, g, nb);
+  else if constexpr (FMT == CQ_Q4_1) load_q41(f, p, g, nb);
+  else if constexpr (FMT == CQ_Q5_1) load_q51(f, p, g, nb);
   else load_q80(f, p, g, nb);
 }
 
@@ -425,6 +504,8 @@ __device__ __forceinline__ void compute_unit(const typename FmtTraits<FMT>::Frag
   else if constexpr (FMT == CQ_Q6_K) compute_q6k<XT>(f, xr, k0, g, acc);
   else if constexpr (FMT == CQ_Q4_0) compute_q40<XT>(f, xr, k0, g, nb, acc);
   else if constexpr (FMT == CQ_Q5_0) compute_q50<XT>(f, xr, k0, g, nb, acc);
+  else if constexpr (FMT == CQ_Q4_1) compute_q41<XT>(f, xr, k0, g, nb, acc);
+  else if constexpr (FMT == CQ_Q5_1) compute_q51<XT>(f, xr, k0, g, nb, acc);
   else compute_q80<XT>(f, xr, k0, g, nb, acc);
 }
 

@@ -218,6 +218,8 @@ __device__ __forceinline__ uint32_t gv1_half(const u4v (&c)[NC], int o) {
 // nibble, (q - 8) * d; Q5_0 (gguf.rs:825-847) adds qh bit j / j + 16 as the
 // 5th bit, (q - 16) * d; Q8_0 (gguf.rs:779-794) q = signed byte j, q * d.
 // The offsets -8 / -16 are applied as -8 / -16 * sum(x) of the block.
+// Q4_1 / Q5_1 (gguf.rs:798-820, 851-874) are Q4_0 / Q5_0 with a min m after
+// the scale and no offset: value = q * d + m, the m term m * sum(x).
 template <int FMT>
 __device__ __forceinline__ float gv1_unit_legacy(const Gv1Block<FMT>& b, const int8_t* xh, const int8_t* xl,
                                                  const int8_t* xe, const float* xs, const float* su) {
@@ -238,14 +240,16 @@ __device__ __forceinline__ float gv1_unit_legacy(const Gv1Block<FMT>& b, const i
         ie = dot4(q, *(const uint32_t*)(xe + xo + 4 * i), ie);
       }
     } else {
-      constexpr int QO = FMT == CQ_Q5_0 ? 6 : 2;  // qs offset in the block
+      constexpr bool Q5 = FMT == CQ_Q5_0 || FMT == CQ_Q5_1;
+      constexpr int HO = FMT == CQ_Q5_1 ? 4 : 2;                                    // qh offset
+      constexpr int QO = FMT == CQ_Q5_0 ? 6 : FMT == CQ_Q4_1 ? 4 : FMT == CQ_Q5_1 ? 8 : 2;  // qs offset
       uint32_t qh = 0;
-      if constexpr (FMT == CQ_Q5_0) qh = gv1_word(b.c, o + 2);
+      if constexpr (Q5) qh = gv1_word(b.c, o + HO);
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const uint32_t w = gv1_word(b.c, o + QO + 4 * i);
         uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-        if constexpr (FMT == CQ_Q5_0) {
+        if constexpr (Q5) {
           lo |= spread4(qh >> (4 * i)) << 4;
           hi |= spread4(qh >> (16 + 4 * i)) << 4;
         }
@@ -262,6 +266,7 @@ __device__ __forceinline__ float gv1_unit_legacy(const Gv1Block<FMT>& b, const i
     if constexpr (FMT == CQ_Q4_0) v = __builtin_fmaf(-8.0f, su[blk], v);
     if constexpr (FMT == CQ_Q5_0) v = __builtin_fmaf(-16.0f, su[blk], v);
     acc = __builtin_fmaf(d, v, acc);
+    if constexpr (FMT == CQ_Q4_1 || FMT == CQ_Q5_1) acc = __builtin_fmaf(f16_bits_to_f32(gv1_half(b.c, o + 2)), su[blk], acc);
   }
   return acc;
 }

@@ -56,7 +56,7 @@ cq_status fail(cq_status st, const char* fmt, ...) {
 
 int block_values(int f) {
   switch (f) {
-    case CQ_Q4_0: case CQ_Q5_0: case CQ_Q8_0: return 32;
+    case CQ_Q4_0: case CQ_Q4_1: case CQ_Q5_0: case CQ_Q5_1: case CQ_Q8_0: return 32;
     case CQ_Q4_K: case CQ_Q5_K: case CQ_Q6_K: return 256;
     default: return 0;
   }
@@ -64,7 +64,9 @@ int block_values(int f) {
 int block_bytes(int f) {
   switch (f) {
     case CQ_Q4_0: return 18;
+    case CQ_Q4_1: return 20;
     case CQ_Q5_0: return 22;
+    case CQ_Q5_1: return 24;
     case CQ_Q8_0: return 34;
     case CQ_Q4_K: return 144;
     case CQ_Q5_K: return 176;
@@ -75,7 +77,9 @@ int block_bytes(int f) {
 const char* fmt_name(int f) {
   switch (f) {
     case CQ_Q4_0: return "q4_0";
+    case CQ_Q4_1: return "q4_1";
     case CQ_Q5_0: return "q5_0";
+    case CQ_Q5_1: return "q5_1";
     case CQ_Q8_0: return "q8_0";
     case CQ_Q4_K: return "q4_k";
     case CQ_Q5_K: return "q5_k";
@@ -91,10 +95,13 @@ int fmt_index(int f) {
     case CQ_Q4_K: return 3;
     case CQ_Q5_K: return 4;
     case CQ_Q6_K: return 5;
+    case CQ_Q4_1: return 6;
+    case CQ_Q5_1: return 7;
     default: return -1;
   }
 }
-const int kFormats[6] = {CQ_Q4_0, CQ_Q5_0, CQ_Q8_0, CQ_Q4_K, CQ_Q5_K, CQ_Q6_K};
+constexpr int kNumFormats = 8;
+const int kFormats[kNumFormats] = {CQ_Q4_0, CQ_Q5_0, CQ_Q8_0, CQ_Q4_K, CQ_Q5_K, CQ_Q6_K, CQ_Q4_1, CQ_Q5_1};
 
 // Kernel argument blocks; layouts match GemvArgs / DequantArgs in the .h files
 // compiled into the code object.
@@ -149,13 +156,13 @@ struct DeviceModule {
   cq_status status = CQ_ERR_NO_DEVICE;
   std::string err;
   hipModule_t mod = nullptr;
-  hipFunction_t gemv[6][2][2] = {};  // [format][x f32][y f16]
-  hipFunction_t dequant[6] = {};
-  hipFunction_t gemm[6][2][2] = {};  // K-quant formats only
-  hipFunction_t gemm2[6][2][2][2] = {};  // [format][NT-1][MT/8-1][y f16], fp16 x
+  hipFunction_t gemv[kNumFormats][2][2] = {};  // [format][x f32][y f16]
+  hipFunction_t dequant[kNumFormats] = {};
+  hipFunction_t gemm[kNumFormats][2][2] = {};  // K-quant formats only
+  hipFunction_t gemm2[kNumFormats][2][2][2] = {};  // [format][NT-1][MT/8-1][y f16], fp16 x
   hipFunction_t xsums = nullptr;
   hipFunction_t reduce[2] = {};       // split-K epilogue [y f16]
-  hipFunction_t gemv1[6][2] = {};     // [format][y f16]
+  hipFunction_t gemv1[kNumFormats][2] = {};     // [format][y f16]
   int cus = 0;                        // compute units of the device
 };
 DeviceModule g_dev[kMaxDevices];
@@ -177,7 +184,7 @@ void load_module(DeviceModule& d, int dev) {
     return;
   }
   char name[96];
-  for (int fi = 0; fi < 6; fi++) {
+  for (int fi = 0; fi < kNumFormats; fi++) {
     const char* fn = fmt_name(kFormats[fi]);
     for (int xt = 0; xt < 2; xt++)
       for (int yt = 0; yt < 2; yt++) {
@@ -212,7 +219,7 @@ void load_module(DeviceModule& d, int dev) {
       return;
     }
   }
-  for (int fi = 0; fi < 6; fi++) {
+  for (int fi = 0; fi < kNumFormats; fi++) {
     for (int yt = 0; yt < 2; yt++) {
       snprintf(name, sizeof name, "cq_gemv1_%s_y%s", fmt_name(kFormats[fi]), yt ? "f16" : "f32");
       if (hipModuleGetFunction(&d.gemv1[fi][yt], d.mod, name) != hipSuccess) {

@@ -27,7 +27,9 @@
   GEMV_KERNEL(cq_gemv_##fname##_xf32_yf16, FMT, 1, 1)
 
 GEMV_FMT(q4_0, CQ_Q4_0)
+GEMV_FMT(q4_1, CQ_Q4_1)
 GEMV_FMT(q5_0, CQ_Q5_0)
+GEMV_FMT(q5_1, CQ_Q5_1)
 GEMV_FMT(q8_0, CQ_Q8_0)
 GEMV_FMT(q4_k, CQ_Q4_K)
 GEMV_FMT(q5_k, CQ_Q5_K)
@@ -40,7 +42,9 @@ GEMV_FMT(q6_k, CQ_Q6_K)
   }
 
 DEQUANT_KERNEL(q4_0, CQ_Q4_0)
+DEQUANT_KERNEL(q4_1, CQ_Q4_1)
 DEQUANT_KERNEL(q5_0, CQ_Q5_0)
+DEQUANT_KERNEL(q5_1, CQ_Q5_1)
 DEQUANT_KERNEL(q8_0, CQ_Q8_0)
 DEQUANT_KERNEL(q4_k, CQ_Q4_K)
 DEQUANT_KERNEL(q5_k, CQ_Q5_K)
@@ -112,6 +116,10 @@ GEMV1_KERNEL(cq_gemv1_q6_k_yf32, CQ_Q6_K, 0)
 GEMV1_KERNEL(cq_gemv1_q6_k_yf16, CQ_Q6_K, 1)
 GEMV1_KERNEL(cq_gemv1_q4_0_yf32, CQ_Q4_0, 0)
 GEMV1_KERNEL(cq_gemv1_q4_0_yf16, CQ_Q4_0, 1)
+GEMV1_KERNEL(cq_gemv1_q4_1_yf32, CQ_Q4_1, 0)
+GEMV1_KERNEL(cq_gemv1_q4_1_yf16, CQ_Q4_1, 1)
+GEMV1_KERNEL(cq_gemv1_q5_1_yf32, CQ_Q5_1, 0)
+GEMV1_KERNEL(cq_gemv1_q5_1_yf16, CQ_Q5_1, 1)
 GEMV1_KERNEL(cq_gemv1_q5_0_yf32, CQ_Q5_0, 0)
 GEMV1_KERNEL(cq_gemv1_q5_0_yf16, CQ_Q5_0, 1)
 GEMV1_KERNEL(cq_gemv1_q8_0_yf32, CQ_Q8_0, 0)

@@ -127,6 +127,46 @@ void quant_q5_0(const float* x, uint8_t* y) {
   memcpy(y + 2, &qh, 4);
 }
 
+// Asymmetric 32-value blocks (ggml quantize_row_q4_1_ref / q5_1_ref):
+// d = (max - min) / (2^bits - 1), m = min, q = round((x - min) / d).
+void quant_q4_1(const float* x, uint8_t* y) {
+  float mn = x[0], mx = x[0];
+  for (int j = 1; j < 32; j++) {
+    mn = std::min(mn, x[j]);
+    mx = std::max(mx, x[j]);
+  }
+  const float d = (mx - mn) / 15.0f;
+  const float id = d ? 1.0f / d : 0.0f;
+  put_f16(y, d);
+  put_f16(y + 2, mn);
+  for (int j = 0; j < 16; j++) {
+    const int a = std::min(15, (int)(int8_t)((x[j] - mn) * id + 0.5f));
+    const int b = std::min(15, (int)(int8_t)((x[16 + j] - mn) * id + 0.5f));
+    y[4 + j] = (uint8_t)(a | (b << 4));
+  }
+}
+
+void quant_q5_1(const float* x, uint8_t* y) {
+  float mn = x[0], mx = x[0];
+  for (int j = 1; j < 32; j++) {
+    mn = std::min(mn, x[j]);
+    mx = std::max(mx, x[j]);
+  }
+  const float d = (mx - mn) / 31.0f;
+  const float id = d ? 1.0f / d : 0.0f;
+  put_f16(y, d);
+  put_f16(y + 2, mn);
+  uint32_t qh = 0;
+  for (int j = 0; j < 16; j++) {
+    const uint32_t a = (uint8_t)((x[j] - mn) * id + 0.5f);
+    const uint32_t b = (uint8_t)((x[16 + j] - mn) * id + 0.5f);
+    y[8 + j] = (uint8_t)((a & 0x0F) | ((b & 0x0F) << 4));
+    qh |= ((a & 0x10) >> 4) << j;
+    qh |= ((b & 0x10) >> 4) << (j + 16);
+  }
+  memcpy(y + 4, &qh, 4);
+}
+
 // ---- K-quant helpers -------------------------------------------------------
 
 // Weighted asymmetric fit of n values to [0, nmax] (ggml make_qkx2_quants).
@@ -396,6 +436,8 @@ extern "C" cq_status cq_quantize(int format, const float* src, int64_t rows, int
   switch (format) {
     case CQ_Q4_0: fn = quant_q4_0; break;
     case CQ_Q5_0: fn = quant_q5_0; break;
+    case CQ_Q4_1: fn = quant_q4_1; break;
+    case CQ_Q5_1: fn = quant_q5_1; break;
     case CQ_Q8_0: fn = quant_q8_0; break;
     case CQ_Q4_K: fn = quant_q4_k; break;
     case CQ_Q5_K: fn = quant_q5_k; break;

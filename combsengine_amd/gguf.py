@@ -39,8 +39,9 @@ META_BOOL, META_STRING, META_ARRAY, META_U64, META_I64, META_F64 = 7, 8, 9, 10, 
 _SCALAR = {META_U8: "<B", META_I8: "<b", META_U16: "<H", META_I16: "<h", META_U32: "<I", META_I32: "<i",
            META_F32: "<f", META_BOOL: "<B", META_U64: "<Q", META_I64: "<q", META_F64: "<d"}
 
-# ggml tensor types served by the quantized path (gguf.rs:1237-1245)
-_GGML_QUANT = {2: QuantFormat.Q4_0, 6: QuantFormat.Q5_0, 8: QuantFormat.Q8_0,
+# ggml tensor types served by the quantized path (gguf.rs:1237-1245), plus
+# Q4_1 (3) and Q5_1 (7), which the reference leaves to its dense path
+_GGML_QUANT = {2: QuantFormat.Q4_0, 3: QuantFormat.Q4_1, 6: QuantFormat.Q5_0, 7: QuantFormat.Q5_1, 8: QuantFormat.Q8_0,
                12: QuantFormat.Q4K, 13: QuantFormat.Q5K, 14: QuantFormat.Q6K}
 
 

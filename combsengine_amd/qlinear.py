@@ -37,9 +37,13 @@ class BadShape(ModelError):
 
 
 class QuantFormat(enum.IntEnum):
-    """combs_formats::QuantFormat (source.rs:42-55); values are GGML type ids."""
+    """combs_formats::QuantFormat (source.rs:42-55); values are GGML type ids.
+    Q4_1 / Q5_1 are served natively here; the reference decodes them only on
+    its dense path (gguf.rs:798-874)."""
     Q4_0 = 2
+    Q4_1 = 3
     Q5_0 = 6
+    Q5_1 = 7
     Q8_0 = 8
     Q4K = 12
     Q5K = 13
@@ -47,6 +51,7 @@ class QuantFormat(enum.IntEnum):
 
 
 _BLOCK = {QuantFormat.Q4_0: (32, 18), QuantFormat.Q5_0: (32, 22), QuantFormat.Q8_0: (32, 34),
+          QuantFormat.Q4_1: (32, 20), QuantFormat.Q5_1: (32, 24),
           QuantFormat.Q4K: (256, 144), QuantFormat.Q5K: (256, 176), QuantFormat.Q6K: (256, 210)}
 
 

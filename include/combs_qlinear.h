@@ -34,10 +34,14 @@ extern "C" {
 #endif
 
 /* GGUF block formats with a device kernel; values are the GGML type ids.
- * Replaces combs_formats::QuantFormat (engine/core/combs-formats/src/source.rs:42-55). */
+ * Replaces combs_formats::QuantFormat (engine/core/combs-formats/src/source.rs:42-55),
+ * plus Q4_1 / Q5_1, which the reference decodes only on its dense path
+ * (gguf.rs:798-820, 851-874, gguf.rs:1194-1196). */
 typedef enum {
   CQ_Q4_0 = 2,  /* 32 values, 18 B: f16 d, 16 nibble bytes          */
+  CQ_Q4_1 = 3,  /* 32 values, 20 B: f16 d, f16 m, 16 nibble bytes   */
   CQ_Q5_0 = 6,  /* 32 values, 22 B: f16 d, u32 high bits, 16 bytes  */
+  CQ_Q5_1 = 7,  /* 32 values, 24 B: f16 d, f16 m, u32 high bits, 16 B */
   CQ_Q8_0 = 8,  /* 32 values, 34 B: f16 d, 32 x i8                  */
   CQ_Q4_K = 12, /* 256 values, 144 B                                */
   CQ_Q5_K = 13, /* 256 values, 176 B                                */

@@ -104,9 +104,14 @@ def ref_matmul(x: np.ndarray, w: np.ndarray) -> np.ndarray:
 
 
 def fused_matmul(fmt: int, data, x: np.ndarray, n: int, k: int) -> np.ndarray:
-    """The reference fused kernels' arithmetic (qmatmul.rs) restated on CPU."""
+    """The reference fused kernels' arithmetic (qmatmul.rs) restated on CPU.
+    Q4_1 / Q5_1 have no fused kernel in the reference: their path is the
+    dense one, dequantise (gguf.rs:798-874) then the f32 matmul
+    (ref_matmul)."""
     buf = np.ascontiguousarray(np.frombuffer(bytes(data), np.uint8) if isinstance(data, (bytes, bytearray)) else data, dtype=np.uint8)
     x = np.ascontiguousarray(x, np.float32)
+    if fmt in (Q4_1, Q5_1):
+        return ref_matmul(x, dequant(fmt, buf, n * k).reshape(n, k))
     m = x.shape[0]
     out = np.empty((m, n), np.float32)
     if lib().orc_fused_matmul(fmt, _p(buf), _p(x), m, n, k, _p(out)) != 0:
@@ -236,7 +241,27 @@ def synth_q8_0(n_blocks: int) -> bytes:
     return b"".join(parts)
 
 
-SYNTH = {Q4_0: synth_q4_0, Q5_0: synth_q5_0, Q8_0: synth_q8_0,
+def synth_q4_1(n_blocks: int) -> bytes:
+    """Not a reference fixture (the reference has no Q4_1 kernel test): the
+    synth_q5_0 construction with a min, d = 0.003*((b%11)+1), m = -8d, then
+    16 LCG bytes."""
+    parts = []
+    for b in range(n_blocks):
+        d = np.float32(0.003) * np.float32((b % 11) + 1.0)
+        parts += [_f16le(d), _f16le(-8 * d), lcg_bytes(16, 0x41D1 ^ b)]
+    return b"".join(parts)
+
+
+def synth_q5_1(n_blocks: int) -> bytes:
+    """As synth_q4_1 for Q5_1: d, m = -16d, then 20 LCG bytes (qh, qs)."""
+    parts = []
+    for b in range(n_blocks):
+        d = np.float32(0.003) * np.float32((b % 11) + 1.0)
+        parts += [_f16le(d), _f16le(-16 * d), lcg_bytes(20, 0x51D1 ^ b)]
+    return b"".join(parts)
+
+
+SYNTH = {Q4_0: synth_q4_0, Q5_0: synth_q5_0, Q8_0: synth_q8_0, Q4_1: synth_q4_1, Q5_1: synth_q5_1,
          Q4_K: synth_q4_k, Q5_K: synth_q5_k, Q6_K: synth_q6_k}
 
 

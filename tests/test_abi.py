@@ -45,8 +45,12 @@ def test_tensor_bytes_and_errors():
     assert out.value == 33030144
     assert L.lib().cq_tensor_bytes(12, 1, 128, ctypes.byref(out)) == L.CQ_ERR_BAD_SHAPE
     assert "multiple of 256" in L.last_error()
-    assert L.lib().cq_tensor_bytes(3, 1, 32, ctypes.byref(out)) == L.CQ_ERR_BAD_FORMAT
-    assert L.lib().cq_block_values(3) == 0
+    # Q4_1 (3) / Q5_1 (7): 20 / 24 bytes per 32 values (gguf.rs:733-735)
+    assert L.lib().cq_tensor_bytes(3, 2, 64, ctypes.byref(out)) == L.CQ_OK and out.value == 80
+    assert L.lib().cq_tensor_bytes(7, 1, 32, ctypes.byref(out)) == L.CQ_OK and out.value == 24
+    # Q4_1's neighbours in the ggml enum are not block formats served here
+    assert L.lib().cq_tensor_bytes(4, 1, 32, ctypes.byref(out)) == L.CQ_ERR_BAD_FORMAT
+    assert L.lib().cq_block_values(4) == 0 and L.lib().cq_block_values(1) == 0
 
 
 @pytest.mark.parametrize("fmt,nbytes,n,k", [

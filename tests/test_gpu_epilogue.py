@@ -80,7 +80,8 @@ def test_bias_none_equals_matmul(cuda):
     assert torch.equal(a, b)
 
 
-PAIRS = [(QuantFormat.Q4K, QuantFormat.Q4K), (QuantFormat.Q4K, QuantFormat.Q6K), (QuantFormat.Q8_0, QuantFormat.Q5_0)]
+PAIRS = [(QuantFormat.Q4K, QuantFormat.Q4K), (QuantFormat.Q4K, QuantFormat.Q6K), (QuantFormat.Q8_0, QuantFormat.Q5_0),
+         (QuantFormat.Q4_1, QuantFormat.Q5_1)]
 
 
 @pytest.mark.parametrize("gf,uf", PAIRS)

@@ -17,8 +17,9 @@ from combsengine_amd import _lib as L
 
 pytestmark = pytest.mark.gpu
 
-FMTS = [QuantFormat.Q4_0, QuantFormat.Q5_0, QuantFormat.Q8_0, QuantFormat.Q4K, QuantFormat.Q5K, QuantFormat.Q6K]
-LEGACY = {QuantFormat.Q4_0, QuantFormat.Q5_0, QuantFormat.Q8_0}
+FMTS = [QuantFormat.Q4_0, QuantFormat.Q5_0, QuantFormat.Q8_0, QuantFormat.Q4K, QuantFormat.Q5K, QuantFormat.Q6K,
+        QuantFormat.Q4_1, QuantFormat.Q5_1]
+LEGACY = {QuantFormat.Q4_0, QuantFormat.Q5_0, QuantFormat.Q8_0, QuantFormat.Q4_1, QuantFormat.Q5_1}
 
 
 def rel_of(fmt):

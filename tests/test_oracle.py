@@ -77,6 +77,37 @@ def test_q5_0_positions():
         assert np.array_equal(v, e)
 
 
+def test_q4_1_positions_and_min():
+    # gguf.rs:798-820: value = q * d + m; d = 0.5, m = -2: low nibble j -> value
+    # j, high nibble -> j + 16; q = 0 gives m exactly.
+    for j in range(16):
+        q = bytearray(16)
+        q[j] = 0x3C  # low 12, high 3
+        v = O.dequant(O.Q4_1, _f16(0.5) + _f16(-2.0) + bytes(q), 32)
+        e = np.full(32, -2.0, np.float32)
+        e[j] = 12 * 0.5 - 2.0
+        e[j + 16] = 3 * 0.5 - 2.0
+        assert np.array_equal(v, e)
+
+
+def test_q5_1_positions_and_min():
+    # gguf.rs:851-874: qh bit i is the 5th bit of value i; d = 1, m = 0.25
+    for i in range(32):
+        qh = (1 << i).to_bytes(4, "little")
+        v = O.dequant(O.Q5_1, _f16(1.0) + _f16(0.25) + qh + bytes([0x21] * 16), 32)
+        e = np.array([1.25] * 16 + [2.25] * 16, np.float32)
+        e[i] += 16.0
+        assert np.array_equal(v, e)
+
+
+def test_q4_1_rounding_order():
+    # q * d rounded, then + m rounded (two f32 roundings, no fused multiply-add):
+    # d = 1 + 2^-10, q = 15, m = 2^-13 -> 15 * d is exact, + m rounds.
+    d, m = np.float16(1 + 2 ** -10), np.float16(2 ** -13)
+    v = O.dequant(O.Q4_1, d.tobytes() + m.tobytes() + bytes([0x0F] + [0] * 15), 32)
+    assert v[0] == np.float32(np.float32(15) * np.float32(d)) + np.float32(m)
+
+
 def test_q8_0_positions_and_sign():
     for j in range(32):
         q = bytearray(32)

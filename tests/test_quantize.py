@@ -50,6 +50,7 @@ def test_q4_0_matches_rule():
 # 7d / 15d, so up to one step (1/8, 1/16 of max|x|); Q8_0: half a step plus the
 # f16 rounding of d.  K-quant bounds are loose empirical envelopes.
 BOUND = {QuantFormat.Q4_0: 1 / 8 + 1e-3, QuantFormat.Q5_0: 1 / 16 + 1e-3, QuantFormat.Q8_0: 1 / 200,
+         QuantFormat.Q4_1: 1 / 15 + 1e-3, QuantFormat.Q5_1: 1 / 31 + 1e-3,
          QuantFormat.Q4K: 1 / 8, QuantFormat.Q5K: 1 / 16, QuantFormat.Q6K: 1 / 40}
 
 

@@ -173,6 +173,28 @@ __device__ __forceinline__ float cq_epilogue(const CqEpi& e, float v, size_t idx
   }
   return v;
 }
+// Epilogue from values loaded beforehand (b = bias[n], u = aux[idx]; unused
+// parts are ignored).  Streaming kernels load them ahead of their weight
+// stream: a load at store time would make the in-order load counter wait for
+// every weight load still in flight.
+__device__ __forceinline__ float cq_epi_apply(const CqEpi& e, float v, float b, float u) {
+  if (e.bias) v += b;
+  if (e.aux) v = cq_act(v, e.act) * u;
+  return v;
+}
+__device__ __forceinline__ float cq_epi_bias(const CqEpi& e, int n) {
+  if (!e.bias) return 0.0f;
+  return e.bias_f16 ? (float)((const _Float16*)e.bias)[n] : ((const float*)e.bias)[n];
+}
+__device__ __forceinline__ float cq_epi_aux(const CqEpi& e, size_t idx) {
+  if (!e.aux) return 0.0f;
+  return e.aux_f16 ? (float)((const _Float16*)e.aux)[idx] : ((const float*)e.aux)[idx];
+}
+template <int YT>
+__device__ __forceinline__ void cq_store_raw(void* y, float v, size_t idx) {
+  if (YT) ((_Float16*)y)[idx] = (_Float16)v;
+  else ((float*)y)[idx] = v;
+}
 // Stores one output element through the epilogue.
 template <int YT>
 __device__ __forceinline__ void cq_store(void* y, const CqEpi& e, float v, size_t idx, int n) {

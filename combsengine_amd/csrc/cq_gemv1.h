@@ -57,6 +57,84 @@ __shared__ float gv_xs[GV1_XMAX / 32];  // s of each 32-value block
 __shared__ float gv_s[GV1_XMAX / 32];   // sum of each 32-value block (fp32 of the fp16 values)
 __shared__ float gv_s16[GV1_XMAX / 16]; // sum of each 16-value half block
 
+// Staging of the fp16 activation row into LDS as three int8 parts per
+// 32-value block (gv_xh/gv_xl/gv_xe), with each block's scale (gv_xs), sum
+// (gv_s) and 16-value half sums (gv_s16).  issue() loads the row into
+// registers (16-byte chunks, thread c holds chunks c, c + 64 NW, ...);
+// commit() quantises and stores them.  Branch-free: indices past the end are
+// clamped, so chunks may be loaded twice with the same value (control-flow
+// joins would make the compiler wait for every outstanding load).  The
+// caller issues its weight loads between the two and synchronises after
+// commit().
+template <int NW>
+struct Gv1XStage {
+  static constexpr int XL = GV1_XMAX / 8 / (64 * NW);  // chunks per thread, at most
+  u4v xv[XL];
+  __device__ __forceinline__ void issue(const _Float16* x, int K) {
+    const int xc_last = K / 8 - 1;
+#pragma unroll
+    for (int i = 0; i < XL; i++) {
+      const int c = min((int)threadIdx.x + 64 * NW * i, xc_last);
+      xv[i] = ld_u128((const uint8_t*)(x + 8 * c));
+    }
+  }
+  // Thread c holds chunk c (8 values); the 4 threads of a 32-value block
+  // share its max and sum.  Threads past the end hold a copy of the last
+  // chunk and store nothing.
+  __device__ __forceinline__ void commit(int K) {
+    const int xc_last = K / 8 - 1;
+#pragma unroll
+    for (int i = 0; i < XL; i++) {
+      if (64 * NW * i > xc_last) break;  // uniform
+      const int craw = (int)threadIdx.x + 64 * NW * i;
+      const int c = min(craw, xc_last);
+      const uint32_t wv[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+      float v[8], mx = 0.0f, sm = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        v[2 * e] = (float)as_h2(wv[e])[0];
+        v[2 * e + 1] = (float)as_h2(wv[e])[1];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        mx = fmaxf(mx, fabsf(v[e]));
+        sm += v[e];
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+      sm += __shfl_xor(sm, 1, 64);
+      const float sm16 = sm;  // this thread pair's 16 values
+      sm += __shfl_xor(sm, 2, 64);
+      const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
+      uint32_t hw[2] = {0, 0}, lw[2] = {0, 0}, ew[2] = {0, 0};
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        // y = x/s in [-127, 127]; residuals after each rounding are in [-0.5, 0.5]
+        const float y = v[e] * inv;
+        const float hv = __builtin_rintf(y);
+        const float r1 = (y - hv) * 254.0f;
+        const float lv = __builtin_rintf(r1);
+        const float ev = __builtin_rintf((r1 - lv) * 254.0f);
+        const int sh = 8 * (e & 3);
+        hw[e >> 2] |= (uint32_t)((int)hv & 0xFF) << sh;
+        lw[e >> 2] |= (uint32_t)((int)lv & 0xFF) << sh;
+        ew[e >> 2] |= (uint32_t)((int)ev & 0xFF) << sh;
+      }
+      if (craw <= xc_last) {
+        const int off = (c >> 5) * GV1_XSTRIDE + 8 * (c & 31);
+        *(u2v*)(gv_xh + off) = u2v{hw[0], hw[1]};
+        *(u2v*)(gv_xl + off) = u2v{lw[0], lw[1]};
+        *(u2v*)(gv_xe + off) = u2v{ew[0], ew[1]};
+        if ((c & 3) == 0) {
+          gv_xs[c >> 2] = mx * (1.0f / 127.0f);
+          gv_s[c >> 2] = sm;
+        }
+        if ((c & 1) == 0) gv_s16[c >> 1] = sm16;
+      }
+    }
+  }
+};
+
 // The 8 scales and mins of a K-quant superblock header as floats.
 __device__ __forceinline__ void gv1_scales(const u4v& hd, float sc[8], float mn[8]) {
 #pragma unroll
@@ -278,7 +356,10 @@ constexpr int gv1_waves() {
   return FMT == CQ_Q4_K || FMT == CQ_Q5_K ? 8 : 4;
 }
 
-template <int FMT, int YT>
+// EPI = 0: no epilogue (a.epi empty), no loads at store time; EPI = 1: the
+// epilogue's loads happen at each store (they wait for the weight loads in
+// flight; a slower path kept for outputs with a bias or a gate).
+template <int FMT, int YT, int EPI>
 __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
   constexpr int NW = gv1_waves<FMT>();
   constexpr int BB = gv1_unit_bytes<FMT>();
@@ -296,73 +377,13 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
   // Load order matters (the vector-memory counter retires in order): the
   // activation chunks first, then the first task's weights, so that staging
   // x into LDS waits only for x while the weights' HBM latency runs on.
-  constexpr int XL = GV1_XMAX / 8 / (64 * NW);  // 16-byte x chunks per thread, at most
-  u4v xv[XL];
-  // (Branch-free: indices past the end are clamped, so chunks may be loaded
-  // and stored twice with the same value; control-flow joins would make the
-  // compiler wait for every outstanding load.)
-  const int xc_last = a.K / 8 - 1;
-#pragma unroll
-  for (int i = 0; i < XL; i++) {
-    const int c = min((int)threadIdx.x + 64 * NW * i, xc_last);
-    xv[i] = ld_u128((const uint8_t*)(a.x + 8 * c));
-  }
+  Gv1XStage<NW> xst;
+  xst.issue(a.x, a.K);
   int t = blockIdx.x * NW + wave;
   Gv1Block<FMT> cur, nxt;
   cur.load(block_ptr(min(t, a.tasks - 1)));
   __builtin_amdgcn_sched_barrier(0);  // keep the weight loads ahead of the staging
-  // Quantise: thread c holds chunk c (8 values); the 4 threads of a 32-value
-  // block share its max and sum.  Threads past the end hold a copy of the
-  // last chunk and store nothing.
-#pragma unroll
-  for (int i = 0; i < XL; i++) {
-    if (64 * NW * i > xc_last) break;  // uniform
-    const int craw = (int)threadIdx.x + 64 * NW * i;
-    const int c = min(craw, xc_last);
-    const uint32_t wv[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
-    float v[8], mx = 0.0f, sm = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      v[2 * e] = (float)as_h2(wv[e])[0];
-      v[2 * e + 1] = (float)as_h2(wv[e])[1];
-    }
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-      mx = fmaxf(mx, fabsf(v[e]));
-      sm += v[e];
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
-    sm += __shfl_xor(sm, 1, 64);
-    const float sm16 = sm;  // this thread pair's 16 values
-    sm += __shfl_xor(sm, 2, 64);
-    const float inv = mx > 0.0f ? 127.0f / mx : 0.0f;
-    uint32_t hw[2] = {0, 0}, lw[2] = {0, 0}, ew[2] = {0, 0};
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-      // y = x/s in [-127, 127]; residuals after each rounding are in [-0.5, 0.5]
-      const float y = v[e] * inv;
-      const float hv = __builtin_rintf(y);
-      const float r1 = (y - hv) * 254.0f;
-      const float lv = __builtin_rintf(r1);
-      const float ev = __builtin_rintf((r1 - lv) * 254.0f);
-      const int sh = 8 * (e & 3);
-      hw[e >> 2] |= (uint32_t)((int)hv & 0xFF) << sh;
-      lw[e >> 2] |= (uint32_t)((int)lv & 0xFF) << sh;
-      ew[e >> 2] |= (uint32_t)((int)ev & 0xFF) << sh;
-    }
-    if (craw <= xc_last) {
-      const int off = (c >> 5) * GV1_XSTRIDE + 8 * (c & 31);
-      *(u2v*)(gv_xh + off) = u2v{hw[0], hw[1]};
-      *(u2v*)(gv_xl + off) = u2v{lw[0], lw[1]};
-      *(u2v*)(gv_xe + off) = u2v{ew[0], ew[1]};
-      if ((c & 3) == 0) {
-        gv_xs[c >> 2] = mx * (1.0f / 127.0f);
-        gv_s[c >> 2] = sm;
-      }
-      if ((c & 1) == 0) gv_s16[c >> 1] = sm16;
-    }
-  }
+  xst.commit(a.K);
   __syncthreads();
 
   auto task_compute = [&](const Gv1Block<FMT>& blk, int tt) {
@@ -381,13 +402,19 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
     if ((a.units & (a.units - 1)) == 0) {
       // a row's lanes form an aligned group of `units` lanes: butterfly within it
       for (int o = a.units >> 1; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
-      if (myunit == 0 && myrow < nrows) cq_store<YT>(a.y, a.epi, part, r0 + myrow, r0 + myrow);
+      if (myunit == 0 && myrow < nrows) {
+        if constexpr (EPI) cq_store<YT>(a.y, a.epi, part, r0 + myrow, r0 + myrow);
+        else cq_store_raw<YT>(a.y, part, r0 + myrow);
+      }
     } else {
       for (int q = 0; q < a.rows; q++) {
         float v = myrow == q ? part : 0.0f;
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-        if (lane == 0 && q < nrows) cq_store<YT>(a.y, a.epi, v, r0 + q, r0 + q);
+        if (lane == 0 && q < nrows) {
+          if constexpr (EPI) cq_store<YT>(a.y, a.epi, v, r0 + q, r0 + q);
+          else cq_store_raw<YT>(a.y, v, r0 + q);
+        }
       }
     }
   };

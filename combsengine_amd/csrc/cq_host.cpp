@@ -143,6 +143,14 @@ struct Gv1Args {
   int N, K, units, rows, tasks;
   CqEpi epi;
 };
+struct Gv2Args {
+  const void* w;
+  const void* x;
+  void* y;
+  long long row_bytes;
+  int N, K, units, R, C, cinv, waves;
+  CqEpi epi;
+};
 struct DequantArgs {
   const void* w;
   float* out;
@@ -162,7 +170,8 @@ struct DeviceModule {
   hipFunction_t gemm2[kNumFormats][2][2][2] = {};  // [format][NT-1][MT/8-1][y f16], fp16 x
   hipFunction_t xsums = nullptr;
   hipFunction_t reduce[2] = {};       // split-K epilogue [y f16]
-  hipFunction_t gemv1[kNumFormats][2] = {};     // [format][y f16]
+  hipFunction_t gemv1[kNumFormats][2][2] = {};  // [format][y f16][epilogue]
+  hipFunction_t gemv2[kNumFormats][2][2] = {};  // K-quants only     // [format][y f16]
   int cus = 0;                        // compute units of the device
 };
 DeviceModule g_dev[kMaxDevices];
@@ -220,13 +229,20 @@ void load_module(DeviceModule& d, int dev) {
     }
   }
   for (int fi = 0; fi < kNumFormats; fi++) {
-    for (int yt = 0; yt < 2; yt++) {
-      snprintf(name, sizeof name, "cq_gemv1_%s_y%s", fmt_name(kFormats[fi]), yt ? "f16" : "f32");
-      if (hipModuleGetFunction(&d.gemv1[fi][yt], d.mod, name) != hipSuccess) {
-        d.err = std::string("missing kernel ") + name;
-        return;
+    for (int yt = 0; yt < 2; yt++)
+      for (int ep = 0; ep < 2; ep++) {
+        snprintf(name, sizeof name, "cq_gemv1_%s_y%s%s", fmt_name(kFormats[fi]), yt ? "f16" : "f32", ep ? "_epi" : "");
+        if (hipModuleGetFunction(&d.gemv1[fi][yt][ep], d.mod, name) != hipSuccess) {
+          d.err = std::string("missing kernel ") + name;
+          return;
+        }
+        if (block_values(kFormats[fi]) != 256) continue;
+        snprintf(name, sizeof name, "cq_gemv2_%s_y%s%s", fmt_name(kFormats[fi]), yt ? "f16" : "f32", ep ? "_epi" : "");
+        if (hipModuleGetFunction(&d.gemv2[fi][yt][ep], d.mod, name) != hipSuccess) {
+          d.err = std::string("missing kernel ") + name;
+          return;
+        }
       }
-    }
   }
   if (hipModuleGetFunction(&d.reduce[0], d.mod, "cq_splitk_reduce_yf32") != hipSuccess ||
       hipModuleGetFunction(&d.reduce[1], d.mod, "cq_splitk_reduce_yf16") != hipSuccess) {
@@ -431,7 +447,44 @@ static cq_status launch_gemv1(DeviceModule* dm, const cq_weight* w, const void* 
   if (cap < 1) cap = 1;
   const int grid = wgs < cap ? wgs : cap;
   void* params[] = {&a};
-  HIP_TRY(hipModuleLaunchKernel(dm->gemv1[fi][yt], (unsigned)grid, 1, 1, 64 * nw, 1, 1, 0, s, params, nullptr));
+  const int ep = epi.bias || epi.aux;
+  HIP_TRY(hipModuleLaunchKernel(dm->gemv1[fi][yt][ep], (unsigned)grid, 1, 1, 64 * nw, 1, 1, 0, s, params, nullptr));
+  return CQ_OK;
+}
+
+// Streaming single-row GEMV for the K-quants (cq_gemv2_*): quarter
+// superblock per lane, steps of 16 superblocks, each wave a contiguous range
+// of rows.  COMBS_GEMV2_WPC sets workgroups (of 8 waves) per compute unit.
+constexpr int kGv2Waves = 8;
+static cq_status launch_gemv2(DeviceModule* dm, const cq_weight* w, const void* x, void* y, int yt, hipStream_t s,
+                              const CqEpi& epi) {
+  const int fi = fmt_index(w->format);
+  Gv2Args a;
+  a.w = w->dev;
+  a.x = x;
+  a.y = y;
+  a.row_bytes = (long long)(w->nbytes / (size_t)w->n);
+  a.N = (int)w->n;
+  a.K = (int)w->k;
+  a.units = (int)(w->k / 256);
+  const bool pow2 = (a.units & (a.units - 1)) == 0;
+  a.R = a.units < 16 && pow2 ? 16 / a.units : 1;
+  a.C = a.R > 1 ? 1 : (a.units + 15) / 16;
+  a.cinv = (65536 + a.C - 1) / a.C;
+  a.epi = epi;
+  int wpc = env_int("COMBS_GEMV2_WPC", 1);
+  if (wpc < 1 || wpc > 2) wpc = 1;
+  // waves: a few steps each where the weight allows, never more than rows
+  const long long row_groups = (a.N + a.R - 1) / a.R;
+  long long grid = (long long)dm->cus * wpc;
+  const long long need = (row_groups + kGv2Waves - 1) / kGv2Waves;
+  if (grid > need) grid = need;
+  a.waves = (int)(grid * kGv2Waves);
+  // per-wave step counts stay far below the 16-bit division trick's range
+  if ((long long)a.N * a.C / a.waves + a.C > 16384) return fail(CQ_ERR_BAD_SHAPE, "gemv2: too many rows per wave");
+  void* params[] = {&a};
+  const int ep = epi.bias || epi.aux;
+  HIP_TRY(hipModuleLaunchKernel(dm->gemv2[fi][yt][ep], (unsigned)grid, 1, 1, 64 * kGv2Waves, 1, 1, 0, s, params, nullptr));
   return CQ_OK;
 }
 
@@ -557,8 +610,14 @@ static cq_status matmul_impl(const cq_weight* w, const void* x, int x_dtype, int
   const bool kq = block_values(w->format) == 256;
   if (kq && (path == CQ_PATH_GEMM || (path == CQ_PATH_AUTO && m > 16)))
     return launch_gemm(dm, w, x, xt, m, y, yt, (hipStream_t)stream, epi);
-  if (m == 1 && !xt && path != CQ_PATH_GEMV && gemv1_fits(w) && env_int("COMBS_GEMV1", 1))
+  if (m == 1 && !xt && path != CQ_PATH_GEMV && gemv1_fits(w) && env_int("COMBS_GEMV1", 1)) {
+    // streaming kernel: Q6_K (measured faster there); COMBS_GEMV2=0 never,
+    // =2 for every K-quant
+    const int g2 = env_int("COMBS_GEMV2", 1);
+    if (kq && (g2 == 2 || (g2 == 1 && w->format == CQ_Q6_K)))
+      return launch_gemv2(dm, w, x, y, yt, (hipStream_t)stream, epi);
     return launch_gemv1(dm, w, x, y, yt, (hipStream_t)stream, epi);
+  }
   return launch_gemv(dm, w, x, xt, m, y, yt, (hipStream_t)stream, epi);
 }
 

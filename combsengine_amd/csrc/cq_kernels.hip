@@ -3,7 +3,8 @@
 // hipModuleLoadData.  Kernel names are extern "C" so the host can look them
 // up with hipModuleGetFunction:
 //   cq_gemv_<fmt>_x<f16|f32>_y<f32|f16>   decode GEMV (m-tiles of 16)
-//   cq_gemv1_<fmt>_y<f32|f16>             decode GEMV, one fp16 activation row
+//   cq_gemv1_<fmt>_y<f32|f16>[_epi]       decode GEMV, one fp16 activation row
+//   cq_gemv2_<fmt>_y<f32|f16>[_epi]       decode GEMV, one fp16 row, streaming (K-quants)
 //   cq_gemm_<fmt>_x<f16|f32>_y<f32|f16>   prefill dequant-GEMM (K-quants)
 //   cq_gemm2_<fmt>_n<1|2>_m<8|16>_y<f32|f16>  prefill dequant-GEMM, large tiles, fp16 x
 //   cq_xsums_f16                          activation sub-block sums for its min term
@@ -11,6 +12,7 @@
 //   cq_dequant_<fmt>                      bit-exact dequantisation
 #include "cq_gemv.h"
 #include "cq_gemv1.h"
+#include "cq_gemv2.h"
 #include "cq_gemm.h"
 #include "cq_gemm2.h"
 #include "cq_dequant.h"
@@ -104,23 +106,37 @@ extern "C" __global__ void __launch_bounds__(256) cq_xsums_f16(const _Float16* x
   xsums_body(x, xs, M, K);
 }
 
-#define GEMV1_KERNEL(NAME, FMT, YT)                                                    \
+#define GEMV1_KERNEL(NAME, FMT, YT, EPI)                                                \
   extern "C" __global__ void __launch_bounds__(64 * gv1_waves<FMT>()) NAME(const Gv1Args a) { \
-    gemv1_body<FMT, YT>(a);                                                            \
+    gemv1_body<FMT, YT, EPI>(a);                                                        \
   }
-GEMV1_KERNEL(cq_gemv1_q4_k_yf32, CQ_Q4_K, 0)
-GEMV1_KERNEL(cq_gemv1_q4_k_yf16, CQ_Q4_K, 1)
-GEMV1_KERNEL(cq_gemv1_q5_k_yf32, CQ_Q5_K, 0)
-GEMV1_KERNEL(cq_gemv1_q5_k_yf16, CQ_Q5_K, 1)
-GEMV1_KERNEL(cq_gemv1_q6_k_yf32, CQ_Q6_K, 0)
-GEMV1_KERNEL(cq_gemv1_q6_k_yf16, CQ_Q6_K, 1)
-GEMV1_KERNEL(cq_gemv1_q4_0_yf32, CQ_Q4_0, 0)
-GEMV1_KERNEL(cq_gemv1_q4_0_yf16, CQ_Q4_0, 1)
-GEMV1_KERNEL(cq_gemv1_q4_1_yf32, CQ_Q4_1, 0)
-GEMV1_KERNEL(cq_gemv1_q4_1_yf16, CQ_Q4_1, 1)
-GEMV1_KERNEL(cq_gemv1_q5_1_yf32, CQ_Q5_1, 0)
-GEMV1_KERNEL(cq_gemv1_q5_1_yf16, CQ_Q5_1, 1)
-GEMV1_KERNEL(cq_gemv1_q5_0_yf32, CQ_Q5_0, 0)
-GEMV1_KERNEL(cq_gemv1_q5_0_yf16, CQ_Q5_0, 1)
-GEMV1_KERNEL(cq_gemv1_q8_0_yf32, CQ_Q8_0, 0)
-GEMV1_KERNEL(cq_gemv1_q8_0_yf16, CQ_Q8_0, 1)
+#define GEMV1_FMT(fname, FMT)                          \
+  GEMV1_KERNEL(cq_gemv1_##fname##_yf32, FMT, 0, 0)     \
+  GEMV1_KERNEL(cq_gemv1_##fname##_yf16, FMT, 1, 0)     \
+  GEMV1_KERNEL(cq_gemv1_##fname##_yf32_epi, FMT, 0, 1) \
+  GEMV1_KERNEL(cq_gemv1_##fname##_yf16_epi, FMT, 1, 1)
+GEMV1_FMT(q4_k, CQ_Q4_K)
+GEMV1_FMT(q5_k, CQ_Q5_K)
+GEMV1_FMT(q6_k, CQ_Q6_K)
+GEMV1_FMT(q4_0, CQ_Q4_0)
+GEMV1_FMT(q4_1, CQ_Q4_1)
+GEMV1_FMT(q5_0, CQ_Q5_0)
+GEMV1_FMT(q5_1, CQ_Q5_1)
+GEMV1_FMT(q8_0, CQ_Q8_0)
+
+#ifndef CQ_GV2_DEPTH
+#define CQ_GV2_DEPTH 3
+#endif
+#define GV2_WAVES 8
+#define GEMV2_KERNEL(NAME, FMT, YT, EPI)                                                        \
+  extern "C" __global__ void __launch_bounds__(64 * GV2_WAVES) NAME(const Gv2Args a) {          \
+    gemv2_body<FMT, YT, GV2_WAVES, CQ_GV2_DEPTH, EPI>(a);                                       \
+  }
+#define GEMV2_FMT(fname, FMT)                          \
+  GEMV2_KERNEL(cq_gemv2_##fname##_yf32, FMT, 0, 0)     \
+  GEMV2_KERNEL(cq_gemv2_##fname##_yf16, FMT, 1, 0)     \
+  GEMV2_KERNEL(cq_gemv2_##fname##_yf32_epi, FMT, 0, 1) \
+  GEMV2_KERNEL(cq_gemv2_##fname##_yf16_epi, FMT, 1, 1)
+GEMV2_FMT(q4_k, CQ_Q4_K)
+GEMV2_FMT(q5_k, CQ_Q5_K)
+GEMV2_FMT(q6_k, CQ_Q6_K)

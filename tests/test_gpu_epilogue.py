@@ -155,3 +155,29 @@ def test_gate_up_rejects_mismatched_shapes(cuda):
     assert st == L.CQ_ERR_BAD_SHAPE and "differ" in L.last_error()
     st = L.lib().cq_matmul_gate_up(a.handle, a.handle, x.data_ptr(), L.CQ_F16, 1, 7, y.data_ptr(), L.CQ_F32, 0)
     assert st == L.CQ_ERR_BAD_SHAPE
+
+
+@pytest.mark.parametrize("fmt", KQ)
+@pytest.mark.parametrize("g2", ["0", "2"])
+@pytest.mark.parametrize("n,k", [(140000, 256), (3000, 512), (700, 4096), (300, 5120)])
+def test_epilogue_single_row_kernels(cuda, monkeypatch, fmt, g2, n, k):
+    """m = 1 epilogues of both single-row kernels: the streaming kernel
+    (COMBS_GEMV2=2) preloads each wave's first 64 rows' bias / gate values and
+    loads the rest at store time (n = 140000 puts ~68 rows on a wave), with R
+    rows per step (k = 256, 512) or several steps per row (k = 5120); the
+    whole-superblock kernel (=0) loads them at store time."""
+    import torch
+    monkeypatch.setenv("COMBS_GEMV2", g2)
+    data, w = _weight(fmt, n, k, 80 + int(fmt))
+    x = _x(1, k, 81)
+    b = np.random.default_rng(82).normal(0, 1, n).astype(np.float32)
+    print(f"single-row epilogue {fmt.name} gemv2={g2} n={n} k={k}", flush=True)
+    y = torch.empty((1, n), device="cuda")
+    w.matmul_bias_into(torch.from_numpy(x).cuda().half(), torch.from_numpy(b).cuda(), y)
+    O.assert_close(y.cpu().numpy(), O.linear(int(fmt), data, x, n, k, b), 1e-3, "bias")
+    # gate(x) * silu: the same weight as gate and up
+    g = gated_up(Activation.Silu, QuantLinearOp(w), QuantLinearOp(w), torch.from_numpy(x).cuda().float().reshape(1, 1, k)
+                 .half())
+    yy = O.fused_matmul(int(fmt), data, x, n, k).astype(np.float64)
+    expect = O.activation(O.ACT_SILU, yy) * yy.astype(np.float16).astype(np.float64)
+    O.assert_close(g.float().cpu().numpy().reshape(1, n), expect, 2e-3, "gate_up")

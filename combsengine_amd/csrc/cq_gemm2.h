@@ -61,12 +61,6 @@ struct LtArgs {
   CqEpi epi;           // applied here, or by the split-K reduction
 };
 
-// Distinct static arrays: the compiler can then see that reading one buffer
-// never aliases a pending DMA into another and inserts no wait for it.
-__shared__ __attribute__((aligned(16))) _Float16 lt_x0[16 * LT_MAXMT * LT_KC];
-__shared__ __attribute__((aligned(16))) _Float16 lt_x1[16 * LT_MAXMT * LT_KC];
-__shared__ __attribute__((aligned(16))) _Float16 lt_s0[16 * LT_MAXMT * 16];
-__shared__ __attribute__((aligned(16))) _Float16 lt_s1[16 * LT_MAXMT * 16];
 
 // 16-byte chunk c (0..15) of a staged row holds K values [8c, 8c+8) of the
 // step.  MFMA step s, lane group g reads chunk lt_chunk; within each 32-lane
@@ -373,6 +367,13 @@ __device__ __forceinline__ void lt_tile(int& bx, int& by) {
 
 template <int FMT, int YT, int NT, int MT>
 __device__ __forceinline__ void gemm2_body(const LtArgs& a) {
+  // Distinct arrays, sized for this MT (so MT = 8 leaves room for two
+  // workgroups per compute unit): the compiler can then see that reading one
+  // buffer never aliases a pending DMA into another and inserts no wait.
+  __shared__ __attribute__((aligned(16))) _Float16 lt_x0[16 * MT * LT_KC];
+  __shared__ __attribute__((aligned(16))) _Float16 lt_x1[16 * MT * LT_KC];
+  __shared__ __attribute__((aligned(16))) _Float16 lt_s0[16 * MT * 16];
+  __shared__ __attribute__((aligned(16))) _Float16 lt_s1[16 * MT * 16];
   LtGemm<FMT, YT, NT, MT> s;
   s.lane = threadIdx.x & 63;
   s.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);

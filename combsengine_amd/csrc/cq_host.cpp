@@ -167,7 +167,7 @@ struct DeviceModule {
   hipFunction_t gemv[kNumFormats][2][2] = {};  // [format][x f32][y f16]
   hipFunction_t dequant[kNumFormats] = {};
   hipFunction_t gemm[kNumFormats][2][2] = {};  // K-quant formats only
-  hipFunction_t gemm2[kNumFormats][2][2][2] = {};  // [format][NT-1][MT/8-1][y f16], fp16 x
+  hipFunction_t gemm2[kNumFormats][3][2][2] = {};  // [format][NT 1/2/4][MT/8-1][y f16], fp16 x
   hipFunction_t xsums = nullptr;
   hipFunction_t reduce[2] = {};       // split-K epilogue [y f16]
   hipFunction_t gemv1[kNumFormats][2][2] = {};  // [format][y f16][epilogue]
@@ -212,11 +212,15 @@ void load_module(DeviceModule& d, int dev) {
             return;
           }
         }
-      for (int nt = 1; nt <= 2; nt++)
+      for (int ni = 0; ni < 3; ni++)
         for (int mt = 8; mt <= 16; mt += 8)
           for (int yt = 0; yt < 2; yt++) {
-            snprintf(name, sizeof name, "cq_gemm2_%s_n%d_m%d_y%s", fn, nt, mt, yt ? "f16" : "f32");
-            if (hipModuleGetFunction(&d.gemm2[fi][nt - 1][mt / 8 - 1][yt], d.mod, name) != hipSuccess) {
+            snprintf(name, sizeof name, "cq_gemm2_%s_n%d_m%d_y%s", fn, 1 << ni, mt, yt ? "f16" : "f32");
+            if (hipModuleGetFunction(&d.gemm2[fi][ni][mt / 8 - 1][yt], d.mod, name) != hipSuccess) {
+              if (ni == 2) {  // NT = 4 is built for some formats only
+                (void)hipGetLastError();  // do not leave the lookup failure for the caller's next check
+                continue;
+              }
               d.err = std::string("missing kernel ") + name;
               return;
             }
@@ -491,8 +495,10 @@ static cq_status launch_gemv2(DeviceModule* dm, const cq_weight* w, const void* 
 // Large-tile prefill GEMM (cq_gemm2_*, fp16 x, K-quants): 4 waves x NT
 // 16-row weight tiles x 16*MT activation rows per workgroup; for Q4_K/Q5_K a
 // cq_xsums_f16 pass first writes the activation sub-block sums its min term
-// uses.  MT = 16 once m exceeds one 128-row block; NT = 2 when that still
-// gives every compute unit a workgroup.  COMBS_GEMM2_NT / COMBS_GEMM2_MT force them.
+// uses.  MT = 8 (128 activation rows): its workgroups fit two per compute
+// unit, which measured faster than MT = 16 at every prefill shape; NT = 2 when
+// that still fills half the workgroup slots.  COMBS_GEMM2_NT / COMBS_GEMM2_MT
+// force them.
 static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* x, int64_t m, void* y, int yt,
                               hipStream_t s, const CqEpi& epi) {
   const int fi = fmt_index(w->format);
@@ -510,10 +516,13 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
   a.usplit = a.units;
   a.epi = epi;
   int mt = env_int("COMBS_GEMM2_MT", 0);
-  if (mt != 8 && mt != 16) mt = m > 128 ? 16 : 8;
+  if (mt != 8 && mt != 16) mt = 8;
+  // MT = 8 workgroups fit two per compute unit (LDS and registers)
+  const long long slots = (long long)dm->cus * (mt == 8 ? 2 : 1);
   const long long mblk = (m + 16 * mt - 1) / (16 * mt);
   int nt = env_int("COMBS_GEMM2_NT", 0);
-  if (nt != 1 && nt != 2) nt = (w->n + 127) / 128 * mblk >= dm->cus ? 2 : 1;
+  if (nt != 1 && nt != 2 && !(nt == 4 && dm->gemm2[fi][2][mt / 8 - 1][yt]))
+    nt = (w->n + 127) / 128 * mblk * 2 >= slots ? 2 : 1;  // NT = 2 while it fills half the slots
   const long long gx = (w->n + 64 * nt - 1) / (64 * nt);
   if (gx > 0x7fffffffLL || mblk > 65535) return fail(CQ_ERR_BAD_SHAPE, "grid too large");
   // Split K when the tiles leave compute units idle (each slice keeps >= 4
@@ -526,7 +535,7 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
   int splits = cs == hipStreamCaptureStatusNone ? env_int("COMBS_GEMM2_SPLIT", 0) : 1;
   if (splits < 1) {
     splits = 1;
-    while (gx * mblk * splits * 2 <= dm->cus && a.units / (splits * 2) >= 4) splits *= 2;
+    while (gx * mblk * splits * 2 <= slots && a.units / (splits * 2) >= 4) splits *= 2;
   }
   if (splits > a.units) splits = a.units;
   a.usplit = (a.units + splits - 1) / splits;
@@ -548,7 +557,7 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
     }
     if (part_bytes) a.part = (float*)((char*)ws + sums_bytes);
     void* params[] = {&a};
-    e = hipModuleLaunchKernel(dm->gemm2[fi][nt - 1][mt / 8 - 1][yt], (unsigned)gx, (unsigned)mblk, (unsigned)splits,
+    e = hipModuleLaunchKernel(dm->gemm2[fi][nt == 4 ? 2 : nt - 1][mt / 8 - 1][yt], (unsigned)gx, (unsigned)mblk, (unsigned)splits,
                               256, 1, 1, 0, s, params, nullptr);
     if (e != hipSuccess || !part_bytes) return e;
     long long mn = m * w->n;

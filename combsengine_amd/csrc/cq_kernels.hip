@@ -66,9 +66,12 @@ GEMM_FMT(q4_k, CQ_Q4_K)
 GEMM_FMT(q5_k, CQ_Q5_K)
 GEMM_FMT(q6_k, CQ_Q6_K)
 
-#define GEMM2_KERNEL(NAME, FMT, YT, NT, MT)                                           \
-  extern "C" __global__ void __launch_bounds__(256) NAME(const LtArgs a) {             \
-    gemm2_body<FMT, YT, NT, MT>(a);                                                    \
+// MT = 8 tiles use 64-72 KB of LDS, so two workgroups share a compute unit
+// when each wave also fits 256 registers (two waves per SIMD).
+#define GEMM2_KERNEL(NAME, FMT, YT, NT, MT)                                                              \
+  extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MT == 8 ? 2 : 1))) \
+  NAME(const LtArgs a) {                                                                                  \
+    gemm2_body<FMT, YT, NT, MT>(a);                                                                       \
   }
 GEMM2_KERNEL(cq_gemm2_q4_k_n1_m8_yf32, CQ_Q4_K, 0, 1, 8)
 GEMM2_KERNEL(cq_gemm2_q4_k_n1_m8_yf16, CQ_Q4_K, 1, 1, 8)

@@ -47,7 +47,6 @@ typedef __attribute__((address_space(1))) void lt_glb_t;
 
 #define LT_KC 128     // K values per step (half a superblock)
 #define LT_MAXMT 16   // activation tiles per workgroup, at most
-#define LT_WAVES 4
 
 struct LtArgs {
   const uint8_t* w;    // packed superblocks, [N rows][row_bytes]
@@ -365,7 +364,7 @@ __device__ __forceinline__ void lt_tile(int& bx, int& by) {
   by = id / nx;
 }
 
-template <int FMT, int YT, int NT, int MT>
+template <int FMT, int YT, int NT, int MT, int NW>
 __device__ __forceinline__ void gemm2_body(const LtArgs& a) {
   // Distinct arrays, sized for this MT (so MT = 8 leaves room for two
   // workgroups per compute unit): the compiler can then see that reading one
@@ -381,7 +380,7 @@ __device__ __forceinline__ void gemm2_body(const LtArgs& a) {
   s.g = s.lane >> 4;
   int bx, by;
   lt_tile(bx, by);
-  const int n0 = (bx * LT_WAVES + s.wave) * 16 * NT;
+  const int n0 = (bx * NW + s.wave) * 16 * NT;
   const int m0 = by * 16 * MT;
   // K slice of this workgroup: superblocks [ub, ub + nu)
   const int ub = blockIdx.z * a.usplit;
@@ -401,7 +400,7 @@ __device__ __forceinline__ void gemm2_body(const LtArgs& a) {
   for (int q = 0; q < 4; q++) s.acol[q] = 16 * (lt_chunk<FMT>(s.g, q) ^ swj);
 
   // Activation DMA: instruction i moves staged rows 4i .. 4i+3 (16 lanes x
-  // 16 B each); this wave issues i = wave + 4 ii.  Lane (row r, slot v)
+  // 16 B each); this wave issues i = wave + NW ii.  Lane (row r, slot v)
   // fetches the row's chunk v ^ lt_sw(r); r & 15 does not depend on ii.
   // 32-bit offsets (M * K * 2 < 2^31 is checked by the host) from a uniform
   // base: the saddr + voffset form of the load.
@@ -412,18 +411,17 @@ __device__ __forceinline__ void gemm2_body(const LtArgs& a) {
   auto dma_x = [&](_Float16* buf, int step) {
     const char* base = (const char*)a.x + (2 * ub + step) * (LT_KC * 2);
 #pragma unroll
-    for (int ii = 0; ii < MT; ii++) {
-      const uint32_t off = min(xoff0 + ii * 16 * K2, xmax);
-      __builtin_amdgcn_global_load_lds((lt_glb_t*)(base + off), (lt_lds_t*)(buf + (s.wave + LT_WAVES * ii) * 512), 16,
-                                       0, 0);
+    for (int ii = 0; ii < 4 * MT / NW; ii++) {
+      const uint32_t off = min(xoff0 + ii * 4 * NW * K2, xmax);
+      __builtin_amdgcn_global_load_lds((lt_glb_t*)(base + off), (lt_lds_t*)(buf + (s.wave + NW * ii) * 512), 16, 0, 0);
     }
   };
   // Sums DMA: 32 rows (2 x 16 B each) per instruction, MT/2 instructions.
   const int srow = s.lane >> 1;
   auto dma_s = [&](_Float16* buf, int u) {
 #pragma unroll
-    for (int ii = 0; ii < (MT + 7) / 8; ii++) {
-      const int i = s.wave + LT_WAVES * ii;
+    for (int ii = 0; ii < (MT / 2 + NW - 1) / NW; ii++) {
+      const int i = s.wave + NW * ii;
       if (i < MT / 2) {
         const int row = min(m0 + 32 * i + srow, a.M - 1);
         const _Float16* src = a.xs + ((size_t)row * a.units + ub + u) * 16 + 8 * (s.lane & 1);

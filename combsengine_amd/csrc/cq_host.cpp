@@ -167,7 +167,7 @@ struct DeviceModule {
   hipFunction_t gemv[kNumFormats][2][2] = {};  // [format][x f32][y f16]
   hipFunction_t dequant[kNumFormats] = {};
   hipFunction_t gemm[kNumFormats][2][2] = {};  // K-quant formats only
-  hipFunction_t gemm2[kNumFormats][3][2][2] = {};  // [format][NT 1/2/4][MT/8-1][y f16], fp16 x
+  hipFunction_t gemm2[kNumFormats][2][2][2] = {};  // [format][NT-1][MT/8-1][y f16], fp16 x
   hipFunction_t xsums = nullptr;
   hipFunction_t reduce[2] = {};       // split-K epilogue [y f16]
   hipFunction_t gemv1[kNumFormats][2][2] = {};  // [format][y f16][epilogue]
@@ -212,15 +212,11 @@ void load_module(DeviceModule& d, int dev) {
             return;
           }
         }
-      for (int ni = 0; ni < 3; ni++)
+      for (int nt = 1; nt <= 2; nt++)
         for (int mt = 8; mt <= 16; mt += 8)
           for (int yt = 0; yt < 2; yt++) {
-            snprintf(name, sizeof name, "cq_gemm2_%s_n%d_m%d_y%s", fn, 1 << ni, mt, yt ? "f16" : "f32");
-            if (hipModuleGetFunction(&d.gemm2[fi][ni][mt / 8 - 1][yt], d.mod, name) != hipSuccess) {
-              if (ni == 2) {  // NT = 4 is built for some formats only
-                (void)hipGetLastError();  // do not leave the lookup failure for the caller's next check
-                continue;
-              }
+            snprintf(name, sizeof name, "cq_gemm2_%s_n%d_m%d_y%s", fn, nt, mt, yt ? "f16" : "f32");
+            if (hipModuleGetFunction(&d.gemm2[fi][nt - 1][mt / 8 - 1][yt], d.mod, name) != hipSuccess) {
               d.err = std::string("missing kernel ") + name;
               return;
             }
@@ -517,13 +513,12 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
   a.epi = epi;
   int mt = env_int("COMBS_GEMM2_MT", 0);
   if (mt != 8 && mt != 16) mt = 8;
-  // MT = 8 workgroups fit two per compute unit (LDS and registers)
-  const long long slots = (long long)dm->cus * (mt == 8 ? 2 : 1);
+  const int nw = 4;  // waves per workgroup (the kernels' launch bounds)
+  const long long slots = (long long)dm->cus * (mt == 8 && nw == 4 ? 2 : 1);
   const long long mblk = (m + 16 * mt - 1) / (16 * mt);
   int nt = env_int("COMBS_GEMM2_NT", 0);
-  if (nt != 1 && nt != 2 && !(nt == 4 && dm->gemm2[fi][2][mt / 8 - 1][yt]))
-    nt = (w->n + 127) / 128 * mblk * 2 >= slots ? 2 : 1;  // NT = 2 while it fills half the slots
-  const long long gx = (w->n + 64 * nt - 1) / (64 * nt);
+  if (nt != 1 && nt != 2) nt = (w->n + 16 * nw - 1) / (16 * nw) * mblk * 2 >= slots ? 2 : 1;  // NT = 2 while it fills half the slots
+  const long long gx = (w->n + 16 * nw * nt - 1) / (16 * nw * nt);
   if (gx > 0x7fffffffLL || mblk > 65535) return fail(CQ_ERR_BAD_SHAPE, "grid too large");
   // Split K when the tiles leave compute units idle (each slice keeps >= 4
   // superblocks); COMBS_GEMM2_SPLIT forces the slice count.
@@ -557,8 +552,8 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
     }
     if (part_bytes) a.part = (float*)((char*)ws + sums_bytes);
     void* params[] = {&a};
-    e = hipModuleLaunchKernel(dm->gemm2[fi][nt == 4 ? 2 : nt - 1][mt / 8 - 1][yt], (unsigned)gx, (unsigned)mblk, (unsigned)splits,
-                              256, 1, 1, 0, s, params, nullptr);
+    hipFunction_t k = dm->gemm2[fi][nt - 1][mt / 8 - 1][yt];
+    e = hipModuleLaunchKernel(k, (unsigned)gx, (unsigned)mblk, (unsigned)splits, 64 * nw, 1, 1, 0, s, params, nullptr);
     if (e != hipSuccess || !part_bytes) return e;
     long long mn = m * w->n;
     int n = (int)w->n;

@@ -17,7 +17,8 @@ value = algorithmic bytes (GGUF-native weight bytes + x + y) of K steps
 
 Also reported: the roofline of the dominant kernel (cq_gemv1_q4_k_yf32, the
 single-row decode GEMV)
-from graphs of single-shape launches, prefill dequant-GEMM TFLOP/s (config 4),
+from graphs of single-shape launches, prefill dequant-GEMM TFLOP/s (config 4,
+eager launches, which may split K),
 lm_head Q6_K and batch 4/16, and the reference CPU path (dequantise once,
 dense f32 GEMV per call) timed on this host as cpu_baseline.
 """
@@ -81,6 +82,27 @@ def graph_time_us(launch, count, reps=3):
     return best, g
 
 
+def eager_time_us(launch, count, reps=3):
+    """Device time per launch (us) of `count` eager launches on the current
+    stream (HIP events around them), best of `reps`.  Used for the prefill
+    GEMMs: each launch runs 30-600 us, so host launch overhead is hidden,
+    and the eager path may split K (captured launches do not)."""
+    import torch
+    launch(0)
+    torch.cuda.synchronize()
+    best = None
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(count):
+            launch(i)
+        b.record()
+        torch.cuda.synchronize()
+        t = a.elapsed_time(b) * 1e3 / count
+        best = t if best is None else min(best, t)
+    return best
+
+
 def load_traffic():
     p = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(p):
@@ -127,7 +149,8 @@ def cpu_baseline(seconds=6.0):
 
 
 def secondary(dev):
-    """Prefill dequant-GEMM (config 4), lm_head Q6_K and batch 4/16 GEMV."""
+    """Prefill dequant-GEMM (config 4, eager launches), lm_head Q6_K and
+    batch 4/16 GEMV (captured graphs)."""
     import numpy as np
     import torch
     from combsengine_amd import QuantFormat
@@ -139,7 +162,7 @@ def secondary(dev):
         for m in (128, 512, 2048):
             x = torch.from_numpy(rng.normal(0, 1, (m, k)).astype(np.float16)).to(dev)
             y = torch.empty((m, n), dtype=torch.float16, device=dev)
-            us, _ = graph_time_us(lambda i: pool[i % len(pool)].matmul_into(x, y), 10 if m < 2048 else 4)
+            us = eager_time_us(lambda i: pool[i % len(pool)].matmul_into(x, y), 20 if m < 2048 else 8)
             fl = 2.0 * m * n * k
             out[f"prefill_{fmt.name}_{n}x{k}_m{m}"] = {"us": round(us, 2), "TFLOPs": round(fl / us / 1e6, 1),
                                                       "frac_fp16_peak": round(fl / us / 1e6 / FP16_PEAK_TFLOPS, 4)}

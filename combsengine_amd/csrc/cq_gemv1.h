@@ -66,7 +66,11 @@ __shared__ float gv_s16[GV1_XMAX / 16]; // sum of each 16-value half block
 // joins would make the compiler wait for every outstanding load).  The
 // caller issues its weight loads between the two and synchronises after
 // commit().
-template <int NW>
+// Q6P = 1 permutes each unit's eight 32-value quadrants (half h, quadrant t)
+// to slot 2 (2h + (t & 1)) + (t >> 1), the layout of cq_gemv2's Q6_K reads
+// (lanes h, c = t & 1 of one slot then fall on different LDS banks); the
+// scale and sum arrays keep the value order.
+template <int NW, int Q6P = 0>
 struct Gv1XStage {
   static constexpr int XL = GV1_XMAX / 8 / (64 * NW);  // chunks per thread, at most
   u4v xv[XL];
@@ -121,7 +125,9 @@ struct Gv1XStage {
         ew[e >> 2] |= (uint32_t)((int)ev & 0xFF) << sh;
       }
       if (craw <= xc_last) {
-        const int off = (c >> 5) * GV1_XSTRIDE + 8 * (c & 31);
+        int q = (c & 31) >> 2;  // quadrant of the unit: 4 h + t
+        if (Q6P) q = 2 * (2 * (q >> 2) + (q & 1)) + ((q >> 1) & 1);
+        const int off = (c >> 5) * GV1_XSTRIDE + 32 * q + 8 * (c & 3);
         *(u2v*)(gv_xh + off) = u2v{hw[0], hw[1]};
         *(u2v*)(gv_xl + off) = u2v{lw[0], lw[1]};
         *(u2v*)(gv_xe + off) = u2v{ew[0], ew[1]};

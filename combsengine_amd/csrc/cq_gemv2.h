@@ -147,7 +147,7 @@ __device__ __forceinline__ float gv2_quarter(const Gv2Frag<FMT>& f, int p, int u
 #pragma unroll
     for (int tt = 0; tt < 2; tt++) {
       const int t = c + 2 * tt;
-      const int ko = ux + 128 * hh + 32 * t;  // staged byte offset of this quadrant
+      const int ko = ux + 64 * (2 * hh + c) + 32 * tt;  // staged byte offset of this quadrant (permuted layout)
       int ih[2] = {0, 0}, il[2] = {0, 0}, ie[2] = {0, 0};
 #pragma unroll
       for (int g = 0; g < 2; g++) {  // 16-value group l/16
@@ -228,7 +228,7 @@ __device__ __forceinline__ void gemv2_body(const Gv2Args& a) {
     pb = cq_epi_bias(a.epi, r);
     pa = cq_epi_aux(a.epi, r);
   }
-  Gv1XStage<NW> xst;
+  Gv1XStage<NW, FMT == CQ_Q6_K> xst;
   xst.issue(a.x, a.K);
   Gv2Frag<FMT> f[D];
   // (unconditional, so that the staging below waits for the x loads only)

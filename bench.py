@@ -18,7 +18,7 @@ value = algorithmic bytes (GGUF-native weight bytes + x + y) of K steps
 Also reported: the roofline of the dominant kernel (cq_gemv1_q4_k_yf32, the
 single-row decode GEMV)
 from graphs of single-shape launches, prefill dequant-GEMM TFLOP/s (config 4,
-eager launches, which may split K),
+the faster of eager launches, which may split K, and a captured graph),
 lm_head Q6_K and batch 4/16, and the reference CPU path (dequantise once,
 dense f32 GEMV per call) timed on this host as cpu_baseline.
 """
@@ -149,8 +149,9 @@ def cpu_baseline(seconds=6.0):
 
 
 def secondary(dev):
-    """Prefill dequant-GEMM (config 4, eager launches), lm_head Q6_K and
-    batch 4/16 GEMV (captured graphs)."""
+    """Prefill dequant-GEMM (config 4: the faster of eager launches, which may
+    split K, and a captured graph, which does not), lm_head Q6_K and batch
+    4/16 GEMV (captured graphs)."""
     import numpy as np
     import torch
     from combsengine_amd import QuantFormat
@@ -162,10 +163,15 @@ def secondary(dev):
         for m in (128, 512, 2048):
             x = torch.from_numpy(rng.normal(0, 1, (m, k)).astype(np.float16)).to(dev)
             y = torch.empty((m, n), dtype=torch.float16, device=dev)
-            us = eager_time_us(lambda i: pool[i % len(pool)].matmul_into(x, y), 20 if m < 2048 else 8)
+            launch = lambda i: pool[i % len(pool)].matmul_into(x, y)  # noqa: E731
+            cnt = 20 if m < 2048 else 8
+            us_e = eager_time_us(launch, cnt)
+            us_g, _ = graph_time_us(launch, cnt)
+            us = min(us_e, us_g)
             fl = 2.0 * m * n * k
             out[f"prefill_{fmt.name}_{n}x{k}_m{m}"] = {"us": round(us, 2), "TFLOPs": round(fl / us / 1e6, 1),
-                                                      "frac_fp16_peak": round(fl / us / 1e6 / FP16_PEAK_TFLOPS, 4)}
+                                                      "frac_fp16_peak": round(fl / us / 1e6 / FP16_PEAK_TFLOPS, 4),
+                                                      "us_eager": round(us_e, 2), "us_graph": round(us_g, 2)}
         del pool
     # lm_head Q6_K [128256 x 4096] (431 MB: larger than the Infinity Cache)
     pool, data = make_pool(QuantFormat.Q6K, 128256, 4096, 2 * 431e6, seed=77)

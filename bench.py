@@ -181,6 +181,29 @@ def secondary(dev):
     b = algo_bytes(data.size, 1, 4096, 128256)
     out["lm_head_q6_k_m1"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1)}
     del pool
+    # gated MLP input at batch 1 (llama.rs:301-303): silu(x.Wg^T) * (x.Wu^T),
+    # one launch over both weights, and the two-launch path for comparison
+    from combsengine_amd import _lib as L
+    gpool, gdata = make_pool(QuantFormat.Q4K, 14336, 4096, 0.6 * (1 << 30), seed=1100)
+    upool, _ = make_pool(QuantFormat.Q4K, 14336, 4096, 0.6 * (1 << 30), seed=1101)
+    x = torch.from_numpy(rng.normal(0, 1, (1, 4096)).astype(np.float16)).to(dev)
+    y = torch.empty((1, 14336), dtype=torch.float16, device=dev)
+
+    def gate_up(i):
+        j = i % len(gpool)
+        st = L.lib().cq_matmul_gate_up(gpool[j].handle, upool[j].handle, x.data_ptr(), L.CQ_F16, 1, L.CQ_ACT_SILU,
+                                       y.data_ptr(), L.CQ_F16, torch.cuda.current_stream().cuda_stream)
+        assert st == L.CQ_OK, L.last_error()
+
+    b = 2 * gdata.size + 4096 * 2 + 14336 * 2
+    res = {}
+    for mode in ("1", "0"):
+        os.environ["COMBS_GATEUP_FUSED"] = mode
+        us, _ = graph_time_us(gate_up, 2 * len(gpool))
+        res["one_launch" if mode == "1" else "two_launches"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1)}
+    os.environ.pop("COMBS_GATEUP_FUSED")
+    out["gate_up_silu_q4_k_14336x4096_m1"] = res
+    del gpool, upool
     # decode batch 4 / 16 on the gate shape
     pool, data = make_pool(QuantFormat.Q4K, 14336, 4096, 0.6 * (1 << 30), seed=1000)
     for m in (4, 16):

@@ -41,12 +41,13 @@
 
 struct Gv1Args {
   const uint8_t* w;
+  const uint8_t* w2;    // EPI = 2: the up projection (same format and shape as w, the gate)
   const _Float16* x;
   void* y;
   long long row_bytes;  // units * block bytes
   int N, K, units;
-  int rows;             // rows per wave task (R)
-  int tasks;            // ceil(N / R)
+  int rows;             // lane rows per wave task (R)
+  int tasks;            // ceil(N / R), or ceil(N / (R / 2)) for EPI = 2
   CqEpi epi;
 };
 
@@ -364,7 +365,11 @@ constexpr int gv1_waves() {
 
 // EPI = 0: no epilogue (a.epi empty), no loads at store time; EPI = 1: the
 // epilogue's loads happen at each store (they wait for the weight loads in
-// flight; a slower path kept for outputs with a bias or a gate).
+// flight; a slower path kept for outputs with a bias or a gate); EPI = 2:
+// the gated MLP input in one launch, y = act(x . W^T) * (x . W2^T) — a task
+// holds R / 2 rows of the gate W and the same R / 2 rows of the up W2 (units
+// a power of two, R >= 2), so both share one activation staging and the
+// product is formed across lanes.
 template <int FMT, int YT, int EPI>
 __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
   constexpr int NW = gv1_waves<FMT>();
@@ -375,7 +380,13 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
   const int myrow = lane / a.units, myunit = lane - myrow * a.units;
   const int stride = gridDim.x * NW;
   // lane's superblock of task t (lanes past the task's rows reread its first)
+  const int half = a.rows >> 1;  // EPI = 2: output rows per task
   auto block_ptr = [&](int t) {
+    if constexpr (EPI == 2) {
+      const int up = myrow >= half;
+      const int row = min(t * half + myrow - (up ? half : 0), a.N - 1);
+      return (up ? a.w2 : a.w) + ((size_t)row * a.units + myunit) * BB;
+    }
     const int r0 = t * a.rows;
     const int nsb = min(a.rows, a.N - r0) * a.units;
     return a.w + ((size_t)r0 * a.units + (lane < nsb ? lane : 0)) * BB;
@@ -393,10 +404,11 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
   __syncthreads();
 
   auto task_compute = [&](const Gv1Block<FMT>& blk, int tt) {
-    const int r0 = tt * a.rows;
-    const int nrows = min(a.rows, a.N - r0);
+    const int r0 = tt * (EPI == 2 ? half : a.rows);
+    const int nrows = min(EPI == 2 ? half : a.rows, a.N - r0);
+    const int rq = EPI == 2 && myrow >= half ? myrow - half : myrow;  // output row of this lane
     float part = 0.0f;
-    if (lane < lanes_used && myrow < nrows) {
+    if (lane < lanes_used && rq < nrows) {
       const int8_t* xh = gv_xh + myunit * GV1_XSTRIDE;
       const int8_t* xl = gv_xl + myunit * GV1_XSTRIDE;
       const int8_t* xe = gv_xe + myunit * GV1_XSTRIDE;
@@ -408,8 +420,13 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
     if ((a.units & (a.units - 1)) == 0) {
       // a row's lanes form an aligned group of `units` lanes: butterfly within it
       for (int o = a.units >> 1; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
-      if (myunit == 0 && myrow < nrows) {
-        if constexpr (EPI) cq_store<YT>(a.y, a.epi, part, r0 + myrow, r0 + myrow);
+      if constexpr (EPI == 2) {
+        // up row rq sits half * units lanes after its gate row
+        const float upv = __shfl(part, (lane + half * a.units) & 63, 64);
+        if (myunit == 0 && myrow < half && rq < nrows)
+          cq_store_raw<YT>(a.y, cq_act(part, a.epi.act) * upv, r0 + rq);
+      } else if (myunit == 0 && myrow < nrows) {
+        if constexpr (EPI == 1) cq_store<YT>(a.y, a.epi, part, r0 + myrow, r0 + myrow);
         else cq_store_raw<YT>(a.y, part, r0 + myrow);
       }
     } else {
@@ -417,8 +434,8 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
         float v = myrow == q ? part : 0.0f;
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-        if (lane == 0 && q < nrows) {
-          if constexpr (EPI) cq_store<YT>(a.y, a.epi, v, r0 + q, r0 + q);
+        if (lane == 0 && q < nrows) {  // (EPI = 2 is launched for power-of-two units only)
+          if constexpr (EPI == 1) cq_store<YT>(a.y, a.epi, v, r0 + q, r0 + q);
           else cq_store_raw<YT>(a.y, v, r0 + q);
         }
       }

@@ -137,6 +137,7 @@ struct LtArgs {
 };
 struct Gv1Args {
   const void* w;
+  const void* w2;
   const void* x;
   void* y;
   long long row_bytes;
@@ -170,7 +171,7 @@ struct DeviceModule {
   hipFunction_t gemm2[kNumFormats][2][2][2] = {};  // [format][NT-1][MT/8-1][y f16], fp16 x
   hipFunction_t xsums = nullptr;
   hipFunction_t reduce[2] = {};       // split-K epilogue [y f16]
-  hipFunction_t gemv1[kNumFormats][2][2] = {};  // [format][y f16][epilogue]
+  hipFunction_t gemv1[kNumFormats][2][3] = {};  // [format][y f16][epilogue: none, general, gated]
   hipFunction_t gemv2[kNumFormats][2][2] = {};  // K-quants only     // [format][y f16]
   int cus = 0;                        // compute units of the device
 };
@@ -230,13 +231,14 @@ void load_module(DeviceModule& d, int dev) {
   }
   for (int fi = 0; fi < kNumFormats; fi++) {
     for (int yt = 0; yt < 2; yt++)
-      for (int ep = 0; ep < 2; ep++) {
-        snprintf(name, sizeof name, "cq_gemv1_%s_y%s%s", fmt_name(kFormats[fi]), yt ? "f16" : "f32", ep ? "_epi" : "");
+      for (int ep = 0; ep < 3; ep++) {
+        static const char* const kEpi[3] = {"", "_epi", "_gated"};
+        snprintf(name, sizeof name, "cq_gemv1_%s_y%s%s", fmt_name(kFormats[fi]), yt ? "f16" : "f32", kEpi[ep]);
         if (hipModuleGetFunction(&d.gemv1[fi][yt][ep], d.mod, name) != hipSuccess) {
           d.err = std::string("missing kernel ") + name;
           return;
         }
-        if (block_values(kFormats[fi]) != 256) continue;
+        if (block_values(kFormats[fi]) != 256 || ep == 2) continue;
         snprintf(name, sizeof name, "cq_gemv2_%s_y%s%s", fmt_name(kFormats[fi]), yt ? "f16" : "f32", ep ? "_epi" : "");
         if (hipModuleGetFunction(&d.gemv2[fi][yt][ep], d.mod, name) != hipSuccess) {
           d.err = std::string("missing kernel ") + name;
@@ -427,11 +429,19 @@ static int gemv1_waves(int format) { return format == CQ_Q4_K || format == CQ_Q5
 static bool gemv1_fits(const cq_weight* w) {
   return w->k % 256 == 0 && w->k <= kGv1MaxK && w->k / 256 <= 64;
 }
+// The one-launch gated gate/up: a task needs >= 2 rows of power-of-two units.
+static bool gemv1_gated_fits(const cq_weight* w) {
+  const int64_t u = w->k / 256;
+  return gemv1_fits(w) && u <= 32 && (u & (u - 1)) == 0;
+}
+// gated (up != null): y = act(x . W^T) * (x . up^T) in one launch; needs
+// K / 256 a power of two up to 32 (gemv1_gated_fits).
 static cq_status launch_gemv1(DeviceModule* dm, const cq_weight* w, const void* x, void* y, int yt, hipStream_t s,
-                              const CqEpi& epi) {
+                              const CqEpi& epi, const cq_weight* up = nullptr) {
   const int fi = fmt_index(w->format);
   Gv1Args a;
   a.w = w->dev;
+  a.w2 = up ? up->dev : nullptr;
   a.x = x;
   a.y = y;
   a.row_bytes = (long long)(w->nbytes / (size_t)w->n);
@@ -439,7 +449,8 @@ static cq_status launch_gemv1(DeviceModule* dm, const cq_weight* w, const void* 
   a.K = (int)w->k;
   a.units = (int)(w->k / 256);
   a.rows = a.units >= 64 ? 1 : 64 / a.units;
-  a.tasks = (int)((w->n + a.rows - 1) / a.rows);
+  const int per_task = up ? a.rows / 2 : a.rows;
+  a.tasks = (int)((w->n + per_task - 1) / per_task);
   a.epi = epi;
   const int nw = gemv1_waves(w->format);
   const int wgs = (a.tasks + nw - 1) / nw;
@@ -447,7 +458,7 @@ static cq_status launch_gemv1(DeviceModule* dm, const cq_weight* w, const void* 
   if (cap < 1) cap = 1;
   const int grid = wgs < cap ? wgs : cap;
   void* params[] = {&a};
-  const int ep = epi.bias || epi.aux;
+  const int ep = up ? 2 : (epi.bias || epi.aux) ? 1 : 0;
   HIP_TRY(hipModuleLaunchKernel(dm->gemv1[fi][yt][ep], (unsigned)grid, 1, 1, 64 * nw, 1, 1, 0, s, params, nullptr));
   return CQ_OK;
 }
@@ -652,6 +663,19 @@ cq_status cq_matmul_gate_up(const cq_weight* gate, const cq_weight* up, const vo
   if (act != CQ_ACT_SILU && act != CQ_ACT_GELU_TANH && act != CQ_ACT_GELU)
     return fail(CQ_ERR_BAD_SHAPE, "unknown activation %d", act);
   const CqEpi none{};
+  // Decode with fp16 x and one format: one launch streams both weights
+  // against one activation staging.  COMBS_GATEUP_FUSED=0 disables it.
+  if (!x || !y) return fail(CQ_ERR_NULL, "NULL x or y");
+  if (y_dtype != CQ_F16 && y_dtype != CQ_F32) return fail(CQ_ERR_BAD_DTYPE, "y_dtype %d", y_dtype);
+  if (m == 1 && x_dtype == CQ_F16 && gate->format == up->format && gemv1_gated_fits(gate) &&
+      env_int("COMBS_GATEUP_FUSED", 1)) {
+    DeviceModule* dm;
+    cq_status st = device_module(&dm);
+    if (st != CQ_OK) return st;
+    CqEpi epi{};
+    epi.act = act;
+    return launch_gemv1(dm, gate, x, y, y_dtype == CQ_F16, (hipStream_t)stream, epi, up);
+  }
   cq_status st = matmul_impl(up, x, x_dtype, m, y, y_dtype, CQ_PATH_AUTO, stream, none);
   if (st != CQ_OK) return st;
   CqEpi epi{};

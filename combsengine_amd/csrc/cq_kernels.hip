@@ -3,7 +3,7 @@
 // hipModuleLoadData.  Kernel names are extern "C" so the host can look them
 // up with hipModuleGetFunction:
 //   cq_gemv_<fmt>_x<f16|f32>_y<f32|f16>   decode GEMV (m-tiles of 16)
-//   cq_gemv1_<fmt>_y<f32|f16>[_epi]       decode GEMV, one fp16 activation row
+//   cq_gemv1_<fmt>_y<f32|f16>[_epi|_gated] decode GEMV, one fp16 activation row
 //   cq_gemv2_<fmt>_y<f32|f16>[_epi]       decode GEMV, one fp16 row, streaming (K-quants)
 //   cq_gemm_<fmt>_x<f16|f32>_y<f32|f16>   prefill dequant-GEMM (K-quants)
 //   cq_gemm2_<fmt>_n<1|2>_m<8|16>_y<f32|f16>  prefill dequant-GEMM, large tiles, fp16 x
@@ -119,7 +119,9 @@ extern "C" __global__ void __launch_bounds__(256) cq_xsums_f16(const _Float16* x
   GEMV1_KERNEL(cq_gemv1_##fname##_yf32, FMT, 0, 0)     \
   GEMV1_KERNEL(cq_gemv1_##fname##_yf16, FMT, 1, 0)     \
   GEMV1_KERNEL(cq_gemv1_##fname##_yf32_epi, FMT, 0, 1) \
-  GEMV1_KERNEL(cq_gemv1_##fname##_yf16_epi, FMT, 1, 1)
+  GEMV1_KERNEL(cq_gemv1_##fname##_yf16_epi, FMT, 1, 1) \
+  GEMV1_KERNEL(cq_gemv1_##fname##_yf32_gated, FMT, 0, 2) \
+  GEMV1_KERNEL(cq_gemv1_##fname##_yf16_gated, FMT, 1, 2)
 GEMV1_FMT(q4_k, CQ_Q4_K)
 GEMV1_FMT(q5_k, CQ_Q5_K)
 GEMV1_FMT(q6_k, CQ_Q6_K)

@@ -181,3 +181,38 @@ def test_epilogue_single_row_kernels(cuda, monkeypatch, fmt, g2, n, k):
     yy = O.fused_matmul(int(fmt), data, x, n, k).astype(np.float64)
     expect = O.activation(O.ACT_SILU, yy) * yy.astype(np.float16).astype(np.float64)
     O.assert_close(g.float().cpu().numpy().reshape(1, n), expect, 2e-3, "gate_up")
+
+
+ALL_FMTS = FMTS + [QuantFormat.Q4_1, QuantFormat.Q5_1]
+
+
+@pytest.mark.parametrize("fmt", ALL_FMTS)
+@pytest.mark.parametrize("n,k", [(300, 4096), (257, 256), (130, 8192), (45, 1024), (97, 3584)])
+@pytest.mark.parametrize("fused", ["1", "0"])
+@pytest.mark.parametrize("y_dt", ["f32", "f16"])
+def test_gate_up_single_row_one_launch(cuda, monkeypatch, fmt, n, k, fused, y_dt):
+    """m = 1, fp16 x, gate and up of one format: the one-launch kernel (both
+    weights against one activation staging, R/2 gate and R/2 up rows per
+    task, ragged last task) for K/256 a power of two up to 32; K = 3584
+    (14 units) and COMBS_GATEUP_FUSED=0 take the two-launch path.  The fused
+    kernel multiplies the fp32 up product (no fp16 rounding in between)."""
+    import torch
+    monkeypatch.setenv("COMBS_GATEUP_FUSED", fused)
+    gd, gw = _weight(fmt, n, k, 90 + int(fmt))
+    ud, uw = _weight(fmt, n, k, 95 + int(fmt))
+    x = _x(1, k, 96)
+    g = O.fused_matmul(int(fmt), gd, x, n, k).astype(np.float64)
+    u = O.fused_matmul(int(fmt), ud, x, n, k).astype(np.float64)
+    one_launch = fused == "1" and (k // 256) & (k // 256 - 1) == 0 and k // 256 <= 32
+    if y_dt == "f16" and not one_launch:
+        u = u.astype(np.float16).astype(np.float64)
+    expect = O.activation(O.ACT_GELU_TANH, g) * u
+    print(f"gate_up m=1 {fmt.name} n={n} k={k} fused={fused} y={y_dt}", flush=True)
+    h = torch.from_numpy(x).cuda().half().reshape(1, 1, k)
+    yt = torch.float32 if y_dt == "f32" else torch.float16
+    y = torch.empty((1, n), dtype=yt, device="cuda")
+    st = L.lib().cq_matmul_gate_up(gw.handle, uw.handle, h.data_ptr(), L.CQ_F16, 1, L.CQ_ACT_GELU_TANH, y.data_ptr(),
+                                   L.CQ_F32 if y_dt == "f32" else L.CQ_F16, 0)
+    assert st == L.CQ_OK, L.last_error()
+    torch.cuda.synchronize()
+    O.assert_close(y.float().cpu().numpy(), expect, 1e-3 if y_dt == "f32" else 2e-3)

@@ -5,35 +5,38 @@
 // Why not the MFMA GEMV here: with one activation row an MFMA computes 16
 // rows of which one is used, and its lane = weight-row layout makes every
 // wave gather 16 separate 16-byte streams.  This kernel gives each lane one
-// whole superblock instead:
+// whole unit (superblock) instead:
 //   - a wave task is R = max(1, 64 / units) consecutive rows, i.e. one
-//     contiguous span of at most 64 superblocks; lane l loads superblock l
-//     of the span (row l / units, unit l % units) straight into registers
-//     (144 / 176 bytes as 16-byte loads; across the wave the loads cover the
-//     span contiguously);
-//   - a persistent grid of one 4-wave workgroup per compute unit, each wave
-//     walking ~N/(R * 4 * CUs) tasks with its loads one task ahead: early
-//     tasks complete early and their arithmetic overlaps the rest of the
-//     stream (issuing every task's loads at once makes all of them arrive
-//     late and serialises memory and compute);
-//   - the inner products are integer: each 32-value activation block is
-//     staged as three int8 parts, x = s * (h + l/254 + e/254^2) with
-//     s = max|x|/127 (about 22 bits relative to the block maximum, error
-//     <= max|x| * 3.9e-8; two parts, 15 bits, fail the 1e-3 bar on outputs
-//     that cancel), and each lane masks its nibbles in place (q = 0..15 /
-//     0..31 per byte) and accumulates v_dot4_i32_i8 against h, l and e,
-//     exactly in int32; per sub-block the three sums become one fp32 value
-//     scaled by d * sc * s, and the min term uses the fp32 sums of the fp16
-//     activations;
-//   - the lanes of a row are summed with cross-lane adds.
-// The activation row is staged once per workgroup in LDS, padded by 16 bytes
-// every 256 values so that lanes reading different units hit different banks.
-// Four int8 multiply-adds per instruction (against two per fp16 dot) roughly
-// halve the VALU work per weight, which is what lets the weight stream run
-// at memory speed.
+//     contiguous span of at most 64 units; lane l computes unit l of the
+//     span (row l / units, unit l % units);
+//   - the span is read as consecutive 16-byte pieces, piece 64 i + l by
+//     lane l in load instruction i, so each instruction is one contiguous
+//     1 KB read (64 strided 16-byte pieces, one unit per lane, measured
+//     8.5 us against 6.6 us for a 33 MB read), and handed to the owning
+//     lanes through a per-wave LDS slice;
+//   - a persistent grid of one 8- or 4-wave workgroup per compute unit,
+//     each wave walking ~N/(R * waves) tasks with the next task's loads in
+//     flight while the current one is computed.
+// Two activation paths:
+//   - Q4_K (the fp16 register path): the row is staged once per workgroup
+//     in LDS as fp16 and every lane keeps its unit's 256 values in registers
+//     for the whole launch (a lane's unit is the same in every task), so the
+//     only LDS traffic per task is the weight hand-over; weights arrive by
+//     LDS DMA into two slices per wave.  Nibbles masked in place are fp16
+//     subnormals q * 2^-24, so v_dot2_f32_f16 forms exact products q * x.
+//   - the other formats: each 32-value activation block is staged as three
+//     int8 parts, x = s * (h + l/254 + e/254^2) with s = max|x|/127 (about
+//     22 bits relative to the block maximum, error <= max|x| * 3.9e-8; two
+//     parts, 15 bits, fail the 1e-3 bar on outputs that cancel), and each
+//     lane masks its nibbles in place (q = 0..15 / 0..31 per byte) and
+//     accumulates v_dot4_i32_i8 against h, l and e, exactly in int32; per
+//     sub-block the three sums become one fp32 value scaled by d * sc * s.
+// In both, the K-quant min term uses fp32 sums of the fp16 activations and
+// the lanes of a row are summed with cross-lane adds.
 // Replaces qmatmul.rs:92-125 (Q4_0), :386-423 (Q5_0), :440-470 (Q8_0),
 // :881-930 (Q4_K), :1064-1117 (Q5_K) and :1184-1229 (Q6_K) for m = 1.
 #pragma once
+#include <type_traits>
 #include "cq_gemv.h"
 
 #define GV1_XMAX 16384                       // largest K staged
@@ -48,6 +51,9 @@ struct Gv1Args {
   int N, K, units;
   int rows;             // lane rows per wave task (R)
   int tasks;            // ceil(N / R), or ceil(N / (R / 2)) for EPI = 2
+  int prefetch2;        // 1: when every wave has at most two tasks, load both before staging x
+  int wave_major;       // 1: task t runs on wave t / grid of workgroup t % grid (balanced), 0: on workgroup t / NW
+  int span;             // 1: load each task as a contiguous span (formats with whole 16-byte units)
   CqEpi epi;
 };
 
@@ -173,7 +179,32 @@ struct Gv1Block {
     for (int i = 0; i < NC; i++) c[i] = ld_u128(p + 16 * i);
     if (TAIL) tail = ld_u16(p + 16 * NC);
   }
+  // Either one unit per lane (span = 0: chunk i of the unit at p), or the
+  // wave's span of units as consecutive 16-byte pieces (span = 1: chunk i
+  // is piece q = 64 i + lane; pieces q < seg come from b0, at most lim0 of
+  // them, the rest from b1, at most lim1; a piece past a limit re-reads the
+  // last valid one).  Both are 16-byte loads; the span form makes each load
+  // instruction one contiguous 1 KB read, which the memory pipeline serves
+  // far faster than 64 strided 16-byte pieces.
+  __device__ __forceinline__ void load_any(bool span, const uint8_t* p, const uint8_t* b0, int seg, int lim0,
+                                           const uint8_t* b1, int lim1) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < NC; i++) {
+      const int q = 64 * i + lane;
+      const uint8_t* sp = q < seg ? b0 + 16 * min(q, lim0 - 1) : b1 + 16 * min(q - seg, lim1 - 1);
+      c[i] = ld_u128(span ? sp : p + 16 * i);
+    }
+    if (TAIL) tail = ld_u16(p + 16 * NC);
+  }
 };
+// Units whose bytes are whole 16-byte chunks can be loaded as a contiguous
+// span and handed to their lanes through LDS (K-quants but Q6_K, and the
+// legacy formats up to 12 chunks; Q8_0's 17 would not fit with 8 waves).
+template <int FMT>
+constexpr bool gv1_spannable() {
+  return gv1_unit_bytes<FMT>() % 16 == 0 && gv1_unit_bytes<FMT>() / 16 <= 12;
+}
 
 __device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
@@ -356,6 +387,127 @@ __device__ __forceinline__ float gv1_unit_legacy(const Gv1Block<FMT>& b, const i
   return acc;
 }
 
+// ---------------------------------------------------------------------------
+// fp16-activation variant (Q4_K): the activation row is staged once per
+// workgroup in LDS as fp16 (a plain copy, with fp32 sums of each 32-value
+// block), and every lane then keeps its unit's 256 values in registers for
+// the whole launch: a lane's unit is lane % units in every task, so after
+// the start the only LDS traffic left is the hand-over of the weight span.
+// The inner products use v_dot2_f32_f16 on nibbles masked in place: in a
+// 16-bit half, q (0..15) or 16 q are the fp16 subnormals q * 2^-24 and
+// 16 q * 2^-24, exact, so each product q * x is exact in fp32.  Masking the
+// word w and w >> 8 pairs bytes (0, 2) and (1, 3), so the lane's values are
+// kept as pairs (x[4m], x[4m+2]) and (x[4m+1], x[4m+3]).
+// Two weight-span slices per wave (8 waves x 64 lanes x 9 chunks each): the
+// next task's pieces land in one by LDS DMA while the other is computed.
+// The fp16 activation row is staged in the second before any DMA uses it.
+#define GV3_SLOT (8 * 64 * 9)
+__shared__ __attribute__((aligned(16))) u4v gv_sa[GV3_SLOT];
+__shared__ __attribute__((aligned(16))) u4v gv_sb[GV3_SLOT];
+typedef __attribute__((address_space(3))) void gv_lds_t;
+typedef __attribute__((address_space(1))) void gv_glb_t;
+
+// LDS DMA of 16 bytes per lane (global_load_lds_dwordx4: lane l's bytes
+// land at LDS byte address m0 + 16 l), issued as inline assembly so that the
+// compiler's wait-count pass does not see it: the kernel waits for these
+// loads itself (gv3_wait_vm), by position in the in-order vector-memory
+// counter.  The compiler treats any pending LDS DMA conservatively and would
+// otherwise wait for every load in flight before each LDS read.
+__device__ __forceinline__ void gv3_dma16(const void* src, uint32_t lds_byte_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+               :
+               : "v"(src), "s"(lds_byte_addr)
+               : "memory", "m0");
+}
+// s_waitcnt vmcnt(N) (other counters unconstrained), then a compiler barrier
+// so that no LDS read moves above it.
+template <int N>
+__device__ __forceinline__ void gv3_wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("" ::: "memory");
+}
+__device__ __forceinline__ uint32_t gv3_lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(gv_lds_t*)p);
+}
+
+// A lane's 256 activations of unit u as the pairs described above
+// (xe[2m] = (x[4m], x[4m+2]), xe[2m+1] = (x[4m+1], x[4m+3])) and its 8
+// block sums.
+struct Gv3XRegs {
+  uint32_t xe[128];
+  float su[8];
+  // x16p: the row with each 256-value unit at a 264-value stride (see below)
+  __device__ __forceinline__ void load(int u, const _Float16* x16p) {
+    const _Float16* src = x16p + 264 * u;
+#pragma unroll
+    for (int q = 0; q < 32; q++) {
+      const u4v v = *(const u4v*)(src + 8 * q);
+      xe[4 * q + 0] = perm(v.y, v.x, 0x05040100u);
+      xe[4 * q + 1] = perm(v.y, v.x, 0x07060302u);
+      xe[4 * q + 2] = perm(v.w, v.z, 0x05040100u);
+      xe[4 * q + 3] = perm(v.w, v.z, 0x07060302u);
+    }
+    // block sums: the pairs of block j are xe[16 j .. 16 j + 15]
+    const h2 one = {1, 1};
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      float a = 0.0f, b = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 16; e += 2) {
+        a = __builtin_amdgcn_fdot2(as_h2(xe[16 * j + e]), one, a, false);
+        b = __builtin_amdgcn_fdot2(as_h2(xe[16 * j + e + 1]), one, b, false);
+      }
+      su[j] = a + b;
+    }
+  }
+};
+
+__device__ __forceinline__ float fdot2u(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
+}
+
+// Q4_K superblock against the lane's registers: per sub-block pair p the
+// low nibbles (sub-block 2p) meet x[64p + j], the high nibbles (2p + 1)
+// x[64p + 32 + j]; sums are in units of 2^-24 (low) and 2^-20 (high).
+__device__ __forceinline__ float gv3_superblock_q4k(const u4v* pc, const Gv3XRegs& xr) {
+  const u4v hd = pc[0];
+  float sc[8], mn[8];
+  gv1_scales(hd, sc, mn);
+  const float d = f16_bits_to_f32(hd.x), dmin = f16_bits_to_f32(hd.x >> 16);
+  float acc = 0.0f, macc = 0.0f;
+#pragma unroll
+  for (int p = 0; p < 4; p++) {
+    float lo0 = 0.0f, lo1 = 0.0f, hi0 = 0.0f, hi1 = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const u4v q = pc[1 + 2 * p + h];
+      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t ws = w[i] >> 8;
+        const int m = 16 * p + 4 * h + i;
+        lo0 = fdot2u(w[i] & 0x000F000Fu, xr.xe[2 * m], lo0);
+        lo1 = fdot2u(ws & 0x000F000Fu, xr.xe[2 * m + 1], lo1);
+        hi0 = fdot2u(w[i] & 0x00F000F0u, xr.xe[2 * m + 16], hi0);
+        hi1 = fdot2u(ws & 0x00F000F0u, xr.xe[2 * m + 17], hi1);
+      }
+    }
+    acc = __builtin_fmaf(sc[2 * p], lo0 + lo1, acc);
+    acc = __builtin_fmaf(sc[2 * p + 1] * 0.0625f, hi0 + hi1, acc);
+    macc = __builtin_fmaf(mn[2 * p], xr.su[2 * p], macc);
+    macc = __builtin_fmaf(mn[2 * p + 1], xr.su[2 * p + 1], macc);
+  }
+  return d * (acc * 16777216.0f) - dmin * macc;
+}
+
+// Activation mode of cq_gemv1 per format: 1 = fp16 registers (Q4_K), 0 =
+// int8 three-part LDS staging.
+template <int FMT>
+constexpr int gv1_xmode() {
+  return FMT == CQ_Q4_K ? 1 : 0;
+}
+
 // Waves per workgroup: 8 (two per SIMD) where the register budget allows it
 // without spilling (Q4_K / Q5_K), else 4.
 template <int FMT>
@@ -370,9 +522,8 @@ constexpr int gv1_waves() {
 // holds R / 2 rows of the gate W and the same R / 2 rows of the up W2 (units
 // a power of two, R >= 2), so both share one activation staging and the
 // product is formed across lanes.
-template <int FMT, int YT, int EPI>
+template <int FMT, int YT, int EPI, int NW = gv1_waves<FMT>(), int XM = gv1_xmode<FMT>()>
 __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
-  constexpr int NW = gv1_waves<FMT>();
   constexpr int BB = gv1_unit_bytes<FMT>();
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -391,32 +542,32 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
     const int nsb = min(a.rows, a.N - r0) * a.units;
     return a.w + ((size_t)r0 * a.units + (lane < nsb ? lane : 0)) * BB;
   };
-  // Load order matters (the vector-memory counter retires in order): the
-  // activation chunks first, then the first task's weights, so that staging
-  // x into LDS waits only for x while the weights' HBM latency runs on.
-  Gv1XStage<NW> xst;
-  xst.issue(a.x, a.K);
-  int t = blockIdx.x * NW + wave;
-  Gv1Block<FMT> cur, nxt;
-  cur.load(block_ptr(min(t, a.tasks - 1)));
-  __builtin_amdgcn_sched_barrier(0);  // keep the weight loads ahead of the staging
-  xst.commit(a.K);
-  __syncthreads();
-
-  auto task_compute = [&](const Gv1Block<FMT>& blk, int tt) {
+  // Span loads: a task's units are R consecutive rows (gate rows then up
+  // rows for EPI = 2), i.e. one or two contiguous byte ranges; each wave
+  // passes its pieces to the owning lanes through its own LDS slice.
+  constexpr bool SPANOK = gv1_spannable<FMT>();
+  constexpr int NC = Gv1Block<FMT>::NC;
+  __shared__ __attribute__((aligned(16))) u4v gv_tw[SPANOK ? NW * 64 * NC : 1];
+  const bool span = SPANOK && (XM == 1 || a.span);
+  auto load_task = [&](Gv1Block<FMT>& blk, int t) {
+    const uint8_t* p = block_ptr(t);
+    if constexpr (EPI == 2) {
+      // lanes [0, half * units) hold gate rows, the rest the same up rows
+      const int r0 = t * half, lim = min(half, a.N - r0) * a.units * NC;
+      const size_t off = (size_t)r0 * a.units * BB;
+      blk.load_any(span, p, a.w + off, half * a.units * NC, lim, a.w2 + off, lim);
+    } else {
+      const int r0 = t * a.rows, lim = min(a.rows, a.N - r0) * a.units * NC;
+      const uint8_t* b0 = a.w + (size_t)r0 * a.units * BB;
+      blk.load_any(span, p, b0, 1 << 30, lim, b0, lim);
+    }
+  };
+  Gv3XRegs xregs;  // XM = 1 only
+  // Row sums across the lanes of each row, then the store (and epilogue).
+  auto task_store = [&](float part, int tt) {
     const int r0 = tt * (EPI == 2 ? half : a.rows);
     const int nrows = min(EPI == 2 ? half : a.rows, a.N - r0);
     const int rq = EPI == 2 && myrow >= half ? myrow - half : myrow;  // output row of this lane
-    float part = 0.0f;
-    if (lane < lanes_used && rq < nrows) {
-      const int8_t* xh = gv_xh + myunit * GV1_XSTRIDE;
-      const int8_t* xl = gv_xl + myunit * GV1_XSTRIDE;
-      const int8_t* xe = gv_xe + myunit * GV1_XSTRIDE;
-      if constexpr (FMT == CQ_Q6_K) part = gv1_superblock_q6k(blk, xh, xl, xe, gv_xs + 8 * myunit, gv_s16 + 16 * myunit);
-      else if constexpr (FmtTraits<FMT>::vals != 256)
-        part = gv1_unit_legacy<FMT>(blk, xh, xl, xe, gv_xs + 8 * myunit, gv_s + 8 * myunit);
-      else part = gv1_superblock<FMT>(blk, xh, xl, xe, gv_xs + 8 * myunit, gv_s + 8 * myunit);
-    }
     if ((a.units & (a.units - 1)) == 0) {
       // a row's lanes form an aligned group of `units` lanes: butterfly within it
       for (int o = a.units >> 1; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
@@ -440,7 +591,142 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
         }
       }
     }
+    };
+  auto task_compute = [&](const Gv1Block<FMT>& blk_in, int tt) {
+    Gv1Block<FMT> blk = blk_in;
+    if constexpr (SPANOK) {
+      if (span) {
+        // piece 64 i + lane -> LDS; then lane reads its unit (pieces NC lane ..)
+        // (one wave's LDS operations complete in order: no barrier needed)
+        u4v* tw = gv_tw + wave * 64 * NC;
+#pragma unroll
+        for (int i = 0; i < NC; i++) tw[64 * i + lane] = blk_in.c[i];
+#pragma unroll
+        for (int i = 0; i < NC; i++) blk.c[i] = tw[NC * lane + i];
+      }
+    }
+    const int r0 = tt * (EPI == 2 ? half : a.rows);
+    const int nrows = min(EPI == 2 ? half : a.rows, a.N - r0);
+    const int rq = EPI == 2 && myrow >= half ? myrow - half : myrow;  // output row of this lane
+    float part = 0.0f;
+    if (lane < lanes_used && rq < nrows) {
+      if constexpr (XM == 1) {
+        part = 0.0f;  // (served by the XM = 1 loop below)
+      } else {
+      const int8_t* xh = gv_xh + myunit * GV1_XSTRIDE;
+      const int8_t* xl = gv_xl + myunit * GV1_XSTRIDE;
+      const int8_t* xe = gv_xe + myunit * GV1_XSTRIDE;
+      if constexpr (FMT == CQ_Q6_K) part = gv1_superblock_q6k(blk, xh, xl, xe, gv_xs + 8 * myunit, gv_s16 + 16 * myunit);
+      else if constexpr (FmtTraits<FMT>::vals != 256)
+        part = gv1_unit_legacy<FMT>(blk, xh, xl, xe, gv_xs + 8 * myunit, gv_s + 8 * myunit);
+      else part = gv1_superblock<FMT>(blk, xh, xl, xe, gv_xs + 8 * myunit, gv_s + 8 * myunit);
+      }
+    }
+    task_store(part, tt);
   };
+  // Load order matters (the vector-memory counter retires in order): the
+  // activation chunks first, then the first task's weights, so that staging
+  // x into LDS waits only for x while the weights' HBM latency runs on.
+  Gv1XStage<NW> xst;  // XM = 0 only
+  if constexpr (XM == 0) xst.issue(a.x, a.K);
+  // Tasks go wave-major over the grid (task t: wave t / grid of workgroup
+  // t % grid), so when tasks do not divide evenly every compute unit still
+  // gets the same share within one task per wave.
+  int t = a.wave_major ? wave * (int)gridDim.x + (int)blockIdx.x : blockIdx.x * NW + wave;
+  if constexpr (XM == 1) {
+    // Each task's span goes straight to LDS by DMA (global_load_lds, 1 KB
+    // per instruction, piece 64 i + lane at 16 (64 i + lane)), two slices
+    // per wave in distinct arrays: task j + 1 lands in one while task j is
+    // computed from the other, its lane reading its superblock at 16 NC lane.
+    static_assert(NW * 64 * NC <= GV3_SLOT, "slot size");
+    const int n = t < a.tasks ? (a.tasks - 1 - t) / stride + 1 : 0;
+    auto dma_task = [&](u4v* arr, int tt) {
+      const uint8_t *b0, *b1;
+      int seg, lim0, lim1;
+      if constexpr (EPI == 2) {
+        const int r0 = tt * half, lim = min(half, a.N - r0) * a.units * NC;
+        const size_t off = (size_t)r0 * a.units * BB;
+        b0 = a.w + off, b1 = a.w2 + off, seg = half * a.units * NC, lim0 = lim1 = lim;
+      } else {
+        const int r0 = tt * a.rows, lim = min(a.rows, a.N - r0) * a.units * NC;
+        b0 = b1 = a.w + (size_t)r0 * a.units * BB, seg = 1 << 30, lim0 = lim1 = lim;
+      }
+      u4v* dst = arr + wave * 64 * NC;
+#pragma unroll
+      for (int i = 0; i < NC; i++) {
+        const int q = 64 * i + lane;
+        const uint8_t* src = q < seg ? b0 + 16 * min(q, lim0 - 1) : b1 + 16 * min(q - seg, lim1 - 1);
+        gv3_dma16(src, gv3_lds_addr(dst + 64 * i));
+      }
+    };
+    auto compute = [&](const u4v* arr, int tt) {
+      const int r0 = tt * (EPI == 2 ? half : a.rows);
+      const int nrows = min(EPI == 2 ? half : a.rows, a.N - r0);
+      const int rq = EPI == 2 && myrow >= half ? myrow - half : myrow;
+      float part = 0.0f;
+      if (lane < lanes_used && rq < nrows) part = gv3_superblock_q4k(arr + wave * 64 * NC + NC * lane, xregs);
+      task_store(part, tt);
+    };
+    static_assert(GV3_SLOT * 16 >= (2 * GV1_XMAX + GV1_XMAX / 32) * 2, "staging fits in gv_sb");
+    // The activation row (K fp16, a multiple of 8 values) goes to gv_sb by
+    // DMA with each 256-value unit at a 264-value (528-byte) stride: units
+    // 512 bytes apart would put every lane's read of the same chunk of its
+    // unit in one LDS bank.  A unit is one half-wave instruction (32 lanes x
+    // 16 bytes); waves take unit pairs in turn.  These DMAs are the older
+    // ones in the counter.
+    _Float16* x16p = (_Float16*)gv_sb;
+    {
+      const int nunits = a.K / 256;
+      for (int u0 = 2 * wave; u0 < nunits; u0 += 2 * NW) {
+        if (lane < 32) gv3_dma16(a.x + 256 * u0 + 8 * lane, gv3_lds_addr(x16p + 264 * u0));
+        if (lane >= 32 && u0 + 1 < nunits)
+          gv3_dma16(a.x + 256 * (u0 + 1) + 8 * (lane - 32), gv3_lds_addr(x16p + 264 * (u0 + 1)) - 512);
+      }
+    }
+    dma_task(gv_sa, min(t, a.tasks - 1));
+    gv3_wait_vm<NC>();
+    __syncthreads();
+    xregs.load(myunit, x16p);
+    __syncthreads();  // the staged row (in gv_sb) fully read before any DMA into gv_sb
+    for (int j = 0; j < n; j += 2, t += 2 * stride) {
+      if (j + 1 < n) {
+        dma_task(gv_sb, t + stride);
+        gv3_wait_vm<NC>();
+      } else {
+        gv3_wait_vm<0>();
+      }
+      compute(gv_sa, t);
+      if (j + 1 >= n) break;
+      if (j + 2 < n) {
+        dma_task(gv_sa, t + 2 * stride);
+        gv3_wait_vm<NC>();
+      } else {
+        gv3_wait_vm<0>();
+      }
+      compute(gv_sb, t + stride);
+    }
+    return;
+  } else {
+  Gv1Block<FMT> cur, nxt;
+  if (a.prefetch2 && a.tasks <= 2 * stride) {
+    // At most two tasks per wave (uniform over the grid): both tasks' loads
+    // go out before the staging, so the whole weight stream is requested at
+    // once; a wave with one task reloads the last task (an L2 hit) and
+    // drops it.
+    load_task(cur, min(t, a.tasks - 1));
+    load_task(nxt, min(t + stride, a.tasks - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    xst.commit(a.K);
+    __syncthreads();
+    if (t < a.tasks) task_compute(cur, t);
+    if (t + stride < a.tasks) task_compute(nxt, t + stride);
+    return;
+  }
+  load_task(cur, min(t, a.tasks - 1));
+  __builtin_amdgcn_sched_barrier(0);  // keep the weight loads ahead of the staging
+  xst.commit(a.K);
+  __syncthreads();
+
   // This wave's tasks t, t + stride, ...: n of them.  Loads run one task
   // ahead of the compute, each compute call sits on a path of its own so
   // that the compiler's in-order load counters wait exactly for the task
@@ -448,10 +734,10 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
   const int n = t < a.tasks ? (a.tasks - 1 - t) / stride + 1 : 0;
   for (int j = 0; j < n; j += 2, t += 2 * stride) {
     if (j + 1 < n) {
-      nxt.load(block_ptr(t + stride));
+      load_task(nxt, t + stride);
       task_compute(cur, t);
       if (j + 2 < n) {
-        cur.load(block_ptr(t + 2 * stride));
+        load_task(cur, t + 2 * stride);
         task_compute(nxt, t + stride);
       } else {
         task_compute(nxt, t + stride);
@@ -459,5 +745,6 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
     } else {
       task_compute(cur, t);
     }
+  }
   }
 }

@@ -141,7 +141,7 @@ struct Gv1Args {
   const void* x;
   void* y;
   long long row_bytes;
-  int N, K, units, rows, tasks;
+  int N, K, units, rows, tasks, prefetch2, wave_major, span;
   CqEpi epi;
 };
 struct Gv2Args {
@@ -150,6 +150,14 @@ struct Gv2Args {
   void* y;
   long long row_bytes;
   int N, K, units, R, C, cinv, waves;
+  CqEpi epi;
+};
+struct GvdArgs {
+  const void* w;
+  const void* x;
+  void* y;
+  long long row_bytes;
+  int M, N, K, units;
   CqEpi epi;
 };
 struct DequantArgs {
@@ -173,6 +181,7 @@ struct DeviceModule {
   hipFunction_t reduce[2] = {};       // split-K epilogue [y f16]
   hipFunction_t gemv1[kNumFormats][2][3] = {};  // [format][y f16][epilogue: none, general, gated]
   hipFunction_t gemv2[kNumFormats][2][2] = {};  // K-quants only     // [format][y f16]
+  hipFunction_t gemvd[kNumFormats][3][2] = {};  // K-quants only: [format][NT 1, 2, 4][y f16]
   int cus = 0;                        // compute units of the device
 };
 DeviceModule g_dev[kMaxDevices];
@@ -238,7 +247,16 @@ void load_module(DeviceModule& d, int dev) {
           d.err = std::string("missing kernel ") + name;
           return;
         }
-        if (block_values(kFormats[fi]) != 256 || ep == 2) continue;
+        if (block_values(kFormats[fi]) != 256) continue;
+        if (ep == 0)
+          for (int nt = 0; nt < 3; nt++) {
+            snprintf(name, sizeof name, "cq_gemvd_%s_n%d_y%s", fmt_name(kFormats[fi]), 1 << nt, yt ? "f16" : "f32");
+            if (hipModuleGetFunction(&d.gemvd[fi][nt][yt], d.mod, name) != hipSuccess) {
+              d.err = std::string("missing kernel ") + name;
+              return;
+            }
+          }
+        if (ep == 2) continue;
         snprintf(name, sizeof name, "cq_gemv2_%s_y%s%s", fmt_name(kFormats[fi]), yt ? "f16" : "f32", ep ? "_epi" : "");
         if (hipModuleGetFunction(&d.gemv2[fi][yt][ep], d.mod, name) != hipSuccess) {
           d.err = std::string("missing kernel ") + name;
@@ -420,6 +438,38 @@ static cq_status launch_gemv(DeviceModule* dm, const cq_weight* w, const void* x
   return CQ_OK;
 }
 
+// Decode GEMV for 2..16 fp16 activation rows, K-quants (cq_gemvd_*):
+// workgroups of 16 * NT weight rows whose nw waves split the superblocks;
+// activation fragments read from global memory (L2), no LDS staging.
+static cq_status launch_gemvd(DeviceModule* dm, const cq_weight* w, const void* x, int64_t m, void* y, int yt,
+                              hipStream_t s, const CqEpi& epi) {
+  const int fi = fmt_index(w->format);
+  GvdArgs a;
+  a.w = w->dev;
+  a.x = x;
+  a.y = y;
+  a.row_bytes = (long long)(w->nbytes / (size_t)w->n);
+  a.M = (int)m;
+  a.N = (int)w->n;
+  a.K = (int)w->k;
+  a.units = (int)(w->k / 256);
+  a.epi = epi;
+  // NT row tiles and nw waves per workgroup (at most one wave per
+  // superblock): 2 and 4 by default, the best measured pair on the Llama-3
+  // shapes at m = 4 / 16 (14.7 / 19.9 us for Q4_K 14336 x 4096).
+  int nt = env_int("COMBS_GVD_NT", 2);
+  if (nt != 1 && nt != 2 && nt != 4) nt = 2;
+  const long long wgs = (w->n + 16 * nt - 1) / (16 * nt);
+  int nw = env_int("COMBS_GVD_WAVES", 4);
+  if (nw < 1 || nw > 8) nw = 4;
+  if (nw > a.units) nw = a.units;
+  if (wgs > 0x7fffffffLL) return fail(CQ_ERR_BAD_SHAPE, "grid too large (n=%lld)", (long long)w->n);
+  void* params[] = {&a};
+  HIP_TRY(hipModuleLaunchKernel(dm->gemvd[fi][nt == 1 ? 0 : nt == 2 ? 1 : 2][yt], (unsigned)wgs, 1, 1, 64 * nw, 1,
+                                1, 0, s, params, nullptr));
+  return CQ_OK;
+}
+
 // Decode GEMV for one fp16 activation row (cq_gemv1_*, every format, K a
 // multiple of 256): wave tasks of max(1, 64/units) whole rows of 256-value
 // units, a persistent grid of one workgroup (8 or 4 waves) per compute unit.  Returns false when the shape is not covered.
@@ -451,6 +501,9 @@ static cq_status launch_gemv1(DeviceModule* dm, const cq_weight* w, const void* 
   a.rows = a.units >= 64 ? 1 : 64 / a.units;
   const int per_task = up ? a.rows / 2 : a.rows;
   a.tasks = (int)((w->n + per_task - 1) / per_task);
+  a.prefetch2 = env_int("COMBS_GEMV1_PREFETCH2", 0);
+  a.span = env_int("COMBS_GEMV1_SPAN", 1);
+  a.wave_major = env_int("COMBS_GEMV1_WAVE_MAJOR", 0);
   a.epi = epi;
   const int nw = gemv1_waves(w->format);
   const int wgs = (a.tasks + nw - 1) / nw;
@@ -633,6 +686,8 @@ static cq_status matmul_impl(const cq_weight* w, const void* x, int x_dtype, int
       return launch_gemv2(dm, w, x, y, yt, (hipStream_t)stream, epi);
     return launch_gemv1(dm, w, x, y, yt, (hipStream_t)stream, epi);
   }
+  if (kq && !xt && m >= 2 && m <= 16 && env_int("COMBS_GEMVD", 1))
+    return launch_gemvd(dm, w, x, m, y, yt, (hipStream_t)stream, epi);
   return launch_gemv(dm, w, x, xt, m, y, yt, (hipStream_t)stream, epi);
 }
 

@@ -5,6 +5,7 @@
 //   cq_gemv_<fmt>_x<f16|f32>_y<f32|f16>   decode GEMV (m-tiles of 16)
 //   cq_gemv1_<fmt>_y<f32|f16>[_epi|_gated] decode GEMV, one fp16 activation row
 //   cq_gemv2_<fmt>_y<f32|f16>[_epi]       decode GEMV, one fp16 row, streaming (K-quants)
+//   cq_gemvd_<fmt>_n<1|2|4>_y<f32|f16>   decode GEMV, 2..16 fp16 rows, direct activations (K-quants)
 //   cq_gemm_<fmt>_x<f16|f32>_y<f32|f16>   prefill dequant-GEMM (K-quants)
 //   cq_gemm2_<fmt>_n<1|2>_m<8|16>_y<f32|f16>  prefill dequant-GEMM, large tiles, fp16 x
 //   cq_xsums_f16                          activation sub-block sums for its min term
@@ -13,6 +14,7 @@
 #include "cq_gemv.h"
 #include "cq_gemv1.h"
 #include "cq_gemv2.h"
+#include "cq_gemvd.h"
 #include "cq_gemm.h"
 #include "cq_gemm2.h"
 #include "cq_dequant.h"
@@ -147,3 +149,21 @@ GEMV1_FMT(q8_0, CQ_Q8_0)
 GEMV2_FMT(q4_k, CQ_Q4_K)
 GEMV2_FMT(q5_k, CQ_Q5_K)
 GEMV2_FMT(q6_k, CQ_Q6_K)
+
+#ifndef CQ_GVD_DEPTH
+#define CQ_GVD_DEPTH 2
+#endif
+#define GEMVD_KERNEL(NAME, FMT, YT, NT)                                                  \
+  extern "C" __global__ void __launch_bounds__(64 * GVD_MAX_WAVES) NAME(const GvdArgs a) { \
+    gemvd_body<FMT, YT, NT, CQ_GVD_DEPTH>(a);                                            \
+  }
+#define GEMVD_FMT(fname, FMT)                          \
+  GEMVD_KERNEL(cq_gemvd_##fname##_n1_yf32, FMT, 0, 1) \
+  GEMVD_KERNEL(cq_gemvd_##fname##_n1_yf16, FMT, 1, 1) \
+  GEMVD_KERNEL(cq_gemvd_##fname##_n2_yf32, FMT, 0, 2) \
+  GEMVD_KERNEL(cq_gemvd_##fname##_n2_yf16, FMT, 1, 2) \
+  GEMVD_KERNEL(cq_gemvd_##fname##_n4_yf32, FMT, 0, 4) \
+  GEMVD_KERNEL(cq_gemvd_##fname##_n4_yf16, FMT, 1, 4)
+GEMVD_FMT(q4_k, CQ_Q4_K)
+GEMVD_FMT(q5_k, CQ_Q5_K)
+GEMVD_FMT(q6_k, CQ_Q6_K)

@@ -329,3 +329,55 @@ def test_graph_capture_replays(cuda, monkeypatch):
         torch.cuda.synchronize()
         assert torch.equal(y, ref), rep
         assert torch.equal(yp, refp), rep
+
+
+@pytest.mark.parametrize("fmt", KQ)
+@pytest.mark.parametrize("nt", ["1", "2", "4"])
+@pytest.mark.parametrize("nw", ["1", "3", "8"])
+@pytest.mark.parametrize("n,k,m", [(300, 4096, 2), (35, 512, 16), (97, 3584, 7), (70, 14336, 4), (33, 256, 16),
+                                   (500, 1792, 9)])
+def test_gemv_batched_direct(cuda, monkeypatch, fmt, nt, nw, n, k, m):
+    """Batched decode (2 <= m <= 16, fp16 x) through the direct-activation
+    kernel: NT row tiles per workgroup (ragged last tile), waves splitting
+    the superblocks (more waves than superblocks, uneven shares, tails
+    shorter than the load pipeline), m not a multiple of 4; checked against
+    the oracle and bit-for-bit stable over repeated launches."""
+    import torch
+    monkeypatch.setenv("COMBS_GVD_NT", nt)
+    monkeypatch.setenv("COMBS_GVD_WAVES", nw)
+    data = synth(fmt, n, k)
+    wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
+    w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
+    x = O.x_pattern(m, k, 13, 31, 15.0, 16.0).reshape(m, k)
+    expect = O.ref_matmul(x, wd)
+    print(f"gemvd {fmt.name} nt={nt} nw={nw} n={n} k={k} m={m}", flush=True)
+    a = _run(w, x, torch.float16, torch.float32)
+    O.assert_close(a, expect, 1e-3, "y32")
+    O.assert_close(_run(w, x, torch.float16, torch.float16), expect, 1e-3, "y16")
+    assert np.array_equal(a.view(np.uint32), _run(w, x, torch.float16, torch.float32).view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", KQ)
+@pytest.mark.parametrize("m", [4, 16])
+def test_gemv_batched_gaussian_llama_shape(cuda, fmt, m):
+    """BASELINE config 3 shape [4096 x 14336] at batch 4 / 16: N(0, 0.02)
+    quantised weights, N(0, 1) fp16 activations, against the oracle, the
+    16-row LDS-staged MFMA kernel and a float64 torch matmul."""
+    import torch
+    rng = np.random.default_rng(300 + int(fmt) + m)
+    n, k = 4096, 14336
+    data = quantize(fmt, rng.normal(0, 0.02, (n, k)).astype(np.float32))
+    wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
+    w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
+    x = rng.normal(0, 1, (m, k)).astype(np.float16).astype(np.float32)
+    print(f"gemvd gaussian {fmt.name} m={m}", flush=True)
+    got = _run(w, x, torch.float16, torch.float32)
+    O.assert_close(got, O.ref_matmul(x, wd), 1e-3, "oracle")
+    f64 = (torch.from_numpy(x).double() @ torch.from_numpy(wd).double().T).numpy()
+    O.assert_close(got, f64, 1e-3, "f64")
+    os.environ["COMBS_GEMVD"] = "0"
+    try:
+        old = _run(w, x, torch.float16, torch.float32)
+    finally:
+        os.environ.pop("COMBS_GEMVD")
+    O.assert_close(got, old, 1e-3, "mfma gemv")

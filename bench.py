@@ -215,6 +215,90 @@ def secondary(dev):
     return out
 
 
+def fast_launcher(pool, x, y):
+    """launch(i): cq_matmul on pool[i % len(pool)] with the arguments resolved
+    once (a ctypes call per launch, no Python-side checks), so that eager
+    bursts stay device-bound."""
+    import torch
+    from combsengine_amd import _lib as L
+    fn = L.lib().cq_matmul_path
+    xt = L.CQ_F16 if x.dtype == torch.float16 else L.CQ_F32
+    yt = L.CQ_F16 if y.dtype == torch.float16 else L.CQ_F32
+    hs = [w.handle for w in pool]
+    xp, yp, m = x.data_ptr(), y.data_ptr(), x.shape[0]
+    s = torch.cuda.current_stream().cuda_stream
+    P = len(hs)
+
+    def launch(i):
+        st = fn(hs[i % P], xp, xt, m, yp, yt, L.CQ_PATH_AUTO, s)
+        if st != L.CQ_OK:
+            raise RuntimeError(L.last_error())
+    return launch
+
+
+def configs_2_3_5(dev):
+    """BASELINE configs 2, 3 and 5 as eager bursts of launches (HIP events
+    around 2 x pool-size launches on the current stream, best of 3), each
+    launch streaming a distinct weight buffer from a pool larger than the
+    Infinity Cache.  Reported per shape: device us per launch and
+    algorithmic GB/s (weight + x + y bytes)."""
+    import numpy as np
+    import torch
+    from combsengine_amd import QuantFormat
+    rng = np.random.default_rng(11)
+    out = {}
+
+    def one(fmt, n, k, m, pool_gib, seed, key, ydt=torch.float32):
+        pool, data = make_pool(fmt, n, k, pool_gib * (1 << 30), seed=seed)
+        res = {}
+        for mm in m:
+            x = torch.from_numpy(rng.normal(0, 1, (mm, k)).astype(np.float16)).to(dev)
+            y = torch.empty((mm, n), dtype=ydt, device=dev)
+            us = eager_time_us(fast_launcher(pool, x, y), max(2 * len(pool), 40))
+            b = algo_bytes(data.size, mm, k, n, ybytes=2 if ydt == torch.float16 else 4)
+            res[f"m{mm}"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1)}
+        out[key] = res
+        del pool
+        return res
+
+    # config 2: Q4_0 / Q8_0 at the Llama-3-8B attention and MLP shapes, batch 1
+    for fmt in (QuantFormat.Q4_0, QuantFormat.Q8_0):
+        for n, k in ((4096, 4096), (14336, 4096), (4096, 14336)):
+            one(fmt, n, k, (1,), 0.6, 2000 + n + k, f"config2_{fmt.name}_{n}x{k}")
+    # config 3: Q4_K / Q5_K projections at batch 1, 4, 16; Q6_K lm_head
+    for fmt in (QuantFormat.Q4K, QuantFormat.Q5K):
+        for n, k in ((14336, 4096), (4096, 14336)):
+            one(fmt, n, k, (1, 4, 16), 0.6, 3000 + n + k, f"config3_{fmt.name}_{n}x{k}")
+    one(QuantFormat.Q6K, 128256, 4096, (1, 4, 16), 0.85, 3100, "config3_Q6K_lm_head_128256x4096")
+    # config 5: one Qwen2.5-7B layer's seven projections (hidden 3584,
+    # intermediate 18944, 4 KV heads x 128); V and down in Q6_K
+    layer = [("q", QuantFormat.Q4K, 3584, 3584), ("k", QuantFormat.Q4K, 512, 3584), ("v", QuantFormat.Q6K, 512, 3584),
+             ("o", QuantFormat.Q4K, 3584, 3584), ("gate", QuantFormat.Q4K, 18944, 3584),
+             ("up", QuantFormat.Q4K, 18944, 3584), ("down", QuantFormat.Q6K, 3584, 18944)]
+    sweep = {}
+    wbytes = 0
+    tot = {1: 0.0, 8: 0.0, 16: 0.0, 512: 0.0}
+    for name, fmt, n, k in layer:
+        pool, data = make_pool(fmt, n, k, 0.4 * (1 << 30), seed=5000 + n + k)
+        wbytes += data.size
+        per = {}
+        for mm in tot:
+            x = torch.from_numpy(rng.normal(0, 1, (mm, k)).astype(np.float16)).to(dev)
+            y = torch.empty((mm, n), dtype=torch.float16 if mm > 16 else torch.float32, device=dev)
+            us = eager_time_us(fast_launcher(pool, x, y), max(2 * len(pool), 40))
+            per[f"m{mm}"] = round(us, 2)
+            tot[mm] += us
+        sweep[name] = per
+        del pool
+    out["config5_qwen2.5_7b_layer"] = {
+        "weight_bytes": wbytes, "us_per_projection": sweep,
+        "layer": {f"m{mm}": {"us": round(t, 2), "weight_GBps": round(wbytes / t / 1e3, 1),
+                             **({"TFLOPs": round(2.0 * mm * sum(n * k for _, _, n, k in layer) / t / 1e6, 1)}
+                                if mm > 16 else {})}
+                  for mm, t in tot.items()}}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -223,6 +307,7 @@ def main():
     ap.add_argument("--pool-gib", type=float, default=1.25)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the BASELINE configs 2 / 3 / 5 sweep")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; multi-GPU sharding of the quantized linear "
@@ -278,6 +363,8 @@ def main():
     traffic_val = round(sum(t_bytes) / len(t_bytes)) if all(t_bytes) else None
 
     extra = {} if args.no_extra else secondary(dev)
+    if not args.no_extra and not args.no_configs:
+        extra["configs"] = configs_2_3_5(dev)
     prefill = {k: v for k, v in extra.items() if k.startswith("prefill_")}
     best_prefill = max((v["TFLOPs"] for v in prefill.values()), default=None)
 

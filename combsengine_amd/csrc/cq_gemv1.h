@@ -432,12 +432,13 @@ __device__ __forceinline__ uint32_t gv3_lds_addr(const void* p) {
 }
 
 // A lane's 256 activations of unit u as the pairs described above
-// (xe[2m] = (x[4m], x[4m+2]), xe[2m+1] = (x[4m+1], x[4m+3])) and its 8
-// block sums.
+// (xe[2m] = (x[4m], x[4m+2]), xe[2m+1] = (x[4m+1], x[4m+3])), read from the
+// staged row x16p (units at a 264-value stride), and its 8 block sums
+// (computed per lane: measured faster than one thread per block through
+// LDS).
 struct Gv3XRegs {
   uint32_t xe[128];
   float su[8];
-  // x16p: the row with each 256-value unit at a 264-value stride (see below)
   __device__ __forceinline__ void load(int u, const _Float16* x16p) {
     const _Float16* src = x16p + 264 * u;
 #pragma unroll
@@ -448,7 +449,9 @@ struct Gv3XRegs {
       xe[4 * q + 2] = perm(v.w, v.z, 0x05040100u);
       xe[4 * q + 3] = perm(v.w, v.z, 0x07060302u);
     }
-    // block sums: the pairs of block j are xe[16 j .. 16 j + 15]
+  }
+  // fp32 sums of the 8 32-value blocks: block j's pairs are xe[16 j .. 16 j + 15]
+  __device__ __forceinline__ void lane_sums() {
     const h2 one = {1, 1};
 #pragma unroll
     for (int j = 0; j < 8; j++) {
@@ -462,7 +465,6 @@ struct Gv3XRegs {
     }
   }
 };
-
 __device__ __forceinline__ float fdot2u(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
 }
@@ -687,6 +689,7 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
     gv3_wait_vm<NC>();
     __syncthreads();
     xregs.load(myunit, x16p);
+    xregs.lane_sums();
     __syncthreads();  // the staged row (in gv_sb) fully read before any DMA into gv_sb
     for (int j = 0; j < n; j += 2, t += 2 * stride) {
       if (j + 1 < n) {

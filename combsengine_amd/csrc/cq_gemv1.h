@@ -398,12 +398,6 @@ __device__ __forceinline__ float gv1_unit_legacy(const Gv1Block<FMT>& b, const i
 // 16 q * 2^-24, exact, so each product q * x is exact in fp32.  Masking the
 // word w and w >> 8 pairs bytes (0, 2) and (1, 3), so the lane's values are
 // kept as pairs (x[4m], x[4m+2]) and (x[4m+1], x[4m+3]).
-// Two weight-span slices per wave (8 waves x 64 lanes x 9 chunks each): the
-// next task's pieces land in one by LDS DMA while the other is computed.
-// The fp16 activation row is staged in the second before any DMA uses it.
-#define GV3_SLOT (8 * 64 * 9)
-__shared__ __attribute__((aligned(16))) u4v gv_sa[GV3_SLOT];
-__shared__ __attribute__((aligned(16))) u4v gv_sb[GV3_SLOT];
 typedef __attribute__((address_space(3))) void gv_lds_t;
 typedef __attribute__((address_space(1))) void gv_glb_t;
 
@@ -438,7 +432,7 @@ __device__ __forceinline__ uint32_t gv3_lds_addr(const void* p) {
 // LDS).
 struct Gv3XRegs {
   uint32_t xe[128];
-  float su[8];
+  float su[16];  // sums of the 16 16-value groups (Q6_K) or of the 8 32-value blocks (Q4_K, su[0..7])
   __device__ __forceinline__ void load(int u, const _Float16* x16p) {
     const _Float16* src = x16p + 264 * u;
 #pragma unroll
@@ -450,21 +444,24 @@ struct Gv3XRegs {
       xe[4 * q + 3] = perm(v.w, v.z, 0x07060302u);
     }
   }
-  // fp32 sums of the 8 32-value blocks: block j's pairs are xe[16 j .. 16 j + 15]
+  // fp32 sums of 16-value groups (G = 16) or 32-value blocks (G = 32):
+  // group j's pairs are xe[G/2 j .. G/2 j + G/2)
+  template <int G>
   __device__ __forceinline__ void lane_sums() {
     const h2 one = {1, 1};
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
+    for (int j = 0; j < 256 / G; j++) {
       float a = 0.0f, b = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 16; e += 2) {
-        a = __builtin_amdgcn_fdot2(as_h2(xe[16 * j + e]), one, a, false);
-        b = __builtin_amdgcn_fdot2(as_h2(xe[16 * j + e + 1]), one, b, false);
+      for (int e = 0; e < G / 2; e += 2) {
+        a = __builtin_amdgcn_fdot2(as_h2(xe[G / 2 * j + e]), one, a, false);
+        b = __builtin_amdgcn_fdot2(as_h2(xe[G / 2 * j + e + 1]), one, b, false);
       }
       su[j] = a + b;
     }
   }
 };
+
 __device__ __forceinline__ float fdot2u(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
 }
@@ -503,11 +500,58 @@ __device__ __forceinline__ float gv3_superblock_q4k(const u4v* pc, const Gv3XReg
   return d * (acc * 16777216.0f) - dmin * macc;
 }
 
+// Q6_K superblock (gguf.rs:968-999) against the lane's registers, read from
+// an LDS slice at any 2-byte alignment (210-byte superblocks; unaligned LDS
+// reads are supported on gfx950).  Value (half hh, quadrant t, l) =
+// (ql nibble | 2 qh bits << 4) - 32 at x[128 hh + 32 t + l] with scale
+// sc[8 hh + l/16 + 2 t]; the 6-bit q of four consecutive l are built as
+// bytes, split into the pairs (l, l+2), (l+1, l+3) as fp16 subnormals, and
+// the -32 is applied as -32 * (sum of the 16-value group).
+__device__ __forceinline__ float gv3_superblock_q6k(const uint8_t* sb, const Gv3XRegs& xr) {
+  const u4v sc0 = ld_u128(sb + 192);
+  const uint32_t scw[4] = {sc0.x, sc0.y, sc0.z, sc0.w};
+  const float d = f16_bits_to_f32(ld_u16(sb + 208));
+  float acc = 0.0f, cacc = 0.0f;
+#pragma unroll
+  for (int hh = 0; hh < 2; hh++) {
+    u4v qh4[2];
+    qh4[0] = ld_u128(sb + 128 + 32 * hh);
+    qh4[1] = ld_u128(sb + 144 + 32 * hh);
+#pragma unroll
+    for (int c = 0; c < 2; c++) {  // ql column: quadrants t = c (low nibbles), c + 2 (high)
+      u4v ql4[2];
+      ql4[0] = ld_u128(sb + 64 * hh + 32 * c);
+      ql4[1] = ld_u128(sb + 64 * hh + 32 * c + 16);
+#pragma unroll
+      for (int tt = 0; tt < 2; tt++) {
+        const int t = c + 2 * tt;
+#pragma unroll
+        for (int g = 0; g < 2; g++) {  // 16-value group l / 16
+          float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+          for (int jj = 0; jj < 4; jj++) {  // l = 16 g + 4 jj .. +3
+            const uint32_t qlw = u4_word(ql4[g], jj), qhw = u4_word(qh4[g], jj);
+            const uint32_t q = ((qlw >> (4 * tt)) & 0x0F0F0F0Fu) | (((qhw >> (2 * t)) & 0x03030303u) << 4);
+            const int m = 32 * hh + 8 * t + 4 * g + jj;
+            s0 = fdot2u(q & 0x00FF00FFu, xr.xe[2 * m], s0);
+            s1 = fdot2u((q >> 8) & 0x00FF00FFu, xr.xe[2 * m + 1], s1);
+          }
+          const int si = 8 * hh + g + 2 * t;
+          const float scf = (float)(int8_t)(scw[si >> 2] >> (8 * (si & 3)));
+          acc = __builtin_fmaf(scf, s0 + s1, acc);
+          cacc = __builtin_fmaf(scf, xr.su[8 * hh + 2 * t + g], cacc);
+        }
+      }
+    }
+  }
+  return d * __builtin_fmaf(16777216.0f, acc, -32.0f * cacc);
+}
+
 // Activation mode of cq_gemv1 per format: 1 = fp16 registers (Q4_K), 0 =
 // int8 three-part LDS staging.
 template <int FMT>
 constexpr int gv1_xmode() {
-  return FMT == CQ_Q4_K ? 1 : 0;
+  return FMT == CQ_Q4_K || FMT == CQ_Q6_K ? 1 : 0;
 }
 
 // Waves per workgroup: 8 (two per SIMD) where the register budget allows it
@@ -524,7 +568,13 @@ constexpr int gv1_waves() {
 // holds R / 2 rows of the gate W and the same R / 2 rows of the up W2 (units
 // a power of two, R >= 2), so both share one activation staging and the
 // product is formed across lanes.
-template <int FMT, int YT, int EPI, int NW = gv1_waves<FMT>(), int XM = gv1_xmode<FMT>()>
+// The gated Q6_K kernel keeps the int8 path and 4 waves.
+template <int FMT, int EPI>
+constexpr int gv1_kernel_waves() {
+  return EPI == 2 && FMT == CQ_Q6_K ? 4 : gv1_waves<FMT>();
+}
+template <int FMT, int YT, int EPI, int NW = gv1_kernel_waves<FMT, EPI>(),
+          int XM = (EPI == 2 && FMT == CQ_Q6_K) ? 0 : gv1_xmode<FMT>()>
 __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
   constexpr int BB = gv1_unit_bytes<FMT>();
   const int lane = threadIdx.x & 63;
@@ -639,26 +689,38 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
     // Each task's span goes straight to LDS by DMA (global_load_lds, 1 KB
     // per instruction, piece 64 i + lane at 16 (64 i + lane)), two slices
     // per wave in distinct arrays: task j + 1 lands in one while task j is
-    // computed from the other, its lane reading its superblock at 16 NC lane.
-    static_assert(NW * 64 * NC <= GV3_SLOT, "slot size");
+    // computed from the other, its lane reading its superblock at BB lane.
+    // A span's last piece may run into the next task's bytes; the host
+    // checks that the weight's byte size is a multiple of 16, so no piece
+    // runs past the weight.
+    // Two span slices per wave (the 64 lanes' units, 64 BB bytes, packed)
+    // in distinct arrays, so the compiler sees reads of one never alias a
+    // DMA into the other.  The fp16 activation row is staged in the second
+    // before any DMA uses it.
+    constexpr int SP = 64 * BB / 16;        // 16-byte pieces per wave slice
+    constexpr int NI = (SP + 63) / 64;      // DMA instructions (1 KB) per task
+    __shared__ __attribute__((aligned(16))) u4v gv_sa[NW * SP];
+    __shared__ __attribute__((aligned(16))) u4v gv_sb[NW * SP];
+    static_assert(NW * SP * 16 >= GV1_XMAX / 256 * 528, "the staged row fits in gv_sb");
     const int n = t < a.tasks ? (a.tasks - 1 - t) / stride + 1 : 0;
     auto dma_task = [&](u4v* arr, int tt) {
       const uint8_t *b0, *b1;
       int seg, lim0, lim1;
       if constexpr (EPI == 2) {
-        const int r0 = tt * half, lim = min(half, a.N - r0) * a.units * NC;
+        // (BB is a multiple of 16 here: EPI = 2 runs this path for Q4_K only)
+        const int r0 = tt * half, lim = min(half, a.N - r0) * a.units * (BB / 16);
         const size_t off = (size_t)r0 * a.units * BB;
-        b0 = a.w + off, b1 = a.w2 + off, seg = half * a.units * NC, lim0 = lim1 = lim;
+        b0 = a.w + off, b1 = a.w2 + off, seg = half * a.units * (BB / 16), lim0 = lim1 = lim;
       } else {
-        const int r0 = tt * a.rows, lim = min(a.rows, a.N - r0) * a.units * NC;
+        const int r0 = tt * a.rows, lim = (min(a.rows, a.N - r0) * a.units * BB + 15) / 16;
         b0 = b1 = a.w + (size_t)r0 * a.units * BB, seg = 1 << 30, lim0 = lim1 = lim;
       }
-      u4v* dst = arr + wave * 64 * NC;
+      u4v* dst = arr + wave * SP;
 #pragma unroll
-      for (int i = 0; i < NC; i++) {
+      for (int i = 0; i < NI; i++) {
         const int q = 64 * i + lane;
         const uint8_t* src = q < seg ? b0 + 16 * min(q, lim0 - 1) : b1 + 16 * min(q - seg, lim1 - 1);
-        gv3_dma16(src, gv3_lds_addr(dst + 64 * i));
+        if (SP % 64 == 0 || i + 1 < NI || q < SP) gv3_dma16(src, gv3_lds_addr(dst + 64 * i));  // the slice ends at SP
       }
     };
     auto compute = [&](const u4v* arr, int tt) {
@@ -666,10 +728,13 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
       const int nrows = min(EPI == 2 ? half : a.rows, a.N - r0);
       const int rq = EPI == 2 && myrow >= half ? myrow - half : myrow;
       float part = 0.0f;
-      if (lane < lanes_used && rq < nrows) part = gv3_superblock_q4k(arr + wave * 64 * NC + NC * lane, xregs);
+      if (lane < lanes_used && rq < nrows) {
+        const uint8_t* sbp = (const uint8_t*)(arr + wave * SP) + BB * lane;
+        if constexpr (FMT == CQ_Q6_K) part = gv3_superblock_q6k(sbp, xregs);
+        else part = gv3_superblock_q4k((const u4v*)sbp, xregs);
+      }
       task_store(part, tt);
     };
-    static_assert(GV3_SLOT * 16 >= (2 * GV1_XMAX + GV1_XMAX / 32) * 2, "staging fits in gv_sb");
     // The activation row (K fp16, a multiple of 8 values) goes to gv_sb by
     // DMA with each 256-value unit at a 264-value (528-byte) stride: units
     // 512 bytes apart would put every lane's read of the same chunk of its
@@ -686,15 +751,15 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
       }
     }
     dma_task(gv_sa, min(t, a.tasks - 1));
-    gv3_wait_vm<NC>();
+    gv3_wait_vm<NI>();
     __syncthreads();
     xregs.load(myunit, x16p);
-    xregs.lane_sums();
+    xregs.lane_sums<FMT == CQ_Q6_K ? 16 : 32>();
     __syncthreads();  // the staged row (in gv_sb) fully read before any DMA into gv_sb
     for (int j = 0; j < n; j += 2, t += 2 * stride) {
       if (j + 1 < n) {
         dma_task(gv_sb, t + stride);
-        gv3_wait_vm<NC>();
+        gv3_wait_vm<NI>();
       } else {
         gv3_wait_vm<0>();
       }
@@ -702,7 +767,7 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
       if (j + 1 >= n) break;
       if (j + 2 < n) {
         dma_task(gv_sa, t + 2 * stride);
-        gv3_wait_vm<NC>();
+        gv3_wait_vm<NI>();
       } else {
         gv3_wait_vm<0>();
       }

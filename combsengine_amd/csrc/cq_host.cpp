@@ -475,9 +475,20 @@ static cq_status launch_gemvd(DeviceModule* dm, const cq_weight* w, const void* 
 // units, a persistent grid of one workgroup (8 or 4 waves) per compute unit.  Returns false when the shape is not covered.
 constexpr int kGv1MaxK = 16384;
 // Waves per cq_gemv1 workgroup (the kernels' launch bounds).
-static int gemv1_waves(int format) { return format == CQ_Q4_K || format == CQ_Q5_K ? 8 : 4; }
+static int gemv1_waves(int format, bool gated) {
+  (void)gated;  // (the gated Q6_K kernel also runs 4 waves)
+  return format == CQ_Q4_K || format == CQ_Q5_K ? 8 : 4;
+}
+// The quarter-superblock kernel (cq_gemv2) stages the row like cq_gemv1's
+// int8 path: K a multiple of 256, at most kGv1MaxK.
+static bool gemv2_fits(const cq_weight* w) { return w->k % 256 == 0 && w->k <= kGv1MaxK; }
 static bool gemv1_fits(const cq_weight* w) {
-  return w->k % 256 == 0 && w->k <= kGv1MaxK && w->k / 256 <= 64;
+  if (!(gemv2_fits(w) && w->k / 256 <= 64)) return false;
+  // Q4_K / Q6_K run the LDS-DMA span path, whose 16-byte pieces must stay
+  // inside the weight: 16-byte aligned, size a multiple of 16
+  if (w->format == CQ_Q4_K || w->format == CQ_Q6_K)
+    return (reinterpret_cast<uintptr_t>(w->dev) & 15) == 0 && w->nbytes % 16 == 0;
+  return true;
 }
 // The one-launch gated gate/up: a task needs >= 2 rows of power-of-two units.
 static bool gemv1_gated_fits(const cq_weight* w) {
@@ -505,7 +516,7 @@ static cq_status launch_gemv1(DeviceModule* dm, const cq_weight* w, const void* 
   a.span = env_int("COMBS_GEMV1_SPAN", 1);
   a.wave_major = env_int("COMBS_GEMV1_WAVE_MAJOR", 0);
   a.epi = epi;
-  const int nw = gemv1_waves(w->format);
+  const int nw = gemv1_waves(w->format, up != nullptr);
   const int wgs = (a.tasks + nw - 1) / nw;
   int cap = env_int("COMBS_GEMV1_GRID", dm->cus);
   if (cap < 1) cap = 1;
@@ -678,13 +689,15 @@ static cq_status matmul_impl(const cq_weight* w, const void* x, int x_dtype, int
   const bool kq = block_values(w->format) == 256;
   if (kq && (path == CQ_PATH_GEMM || (path == CQ_PATH_AUTO && m > 16)))
     return launch_gemm(dm, w, x, xt, m, y, yt, (hipStream_t)stream, epi);
-  if (m == 1 && !xt && path != CQ_PATH_GEMV && gemv1_fits(w) && env_int("COMBS_GEMV1", 1)) {
-    // streaming kernel: Q6_K (measured faster there); COMBS_GEMV2=0 never,
-    // =2 for every K-quant
-    const int g2 = env_int("COMBS_GEMV2", 1);
-    if (kq && (g2 == 2 || (g2 == 1 && w->format == CQ_Q6_K)))
+  if (m == 1 && !xt && path != CQ_PATH_GEMV && env_int("COMBS_GEMV1", 1)) {
+    // quarter-superblock streaming kernel (cq_gemv2): COMBS_GEMV2=2 for
+    // every K-quant, =1 for Q6_K, 0 (default) only where cq_gemv1 does not
+    // fit (a K-quant weight whose bytes are not 16-byte aligned)
+    const int g2 = env_int("COMBS_GEMV2", 0);
+    if (kq && (g2 == 2 || (g2 == 1 && w->format == CQ_Q6_K)) && gemv2_fits(w))
       return launch_gemv2(dm, w, x, y, yt, (hipStream_t)stream, epi);
-    return launch_gemv1(dm, w, x, y, yt, (hipStream_t)stream, epi);
+    if (gemv1_fits(w)) return launch_gemv1(dm, w, x, y, yt, (hipStream_t)stream, epi);
+    if (kq && w->k / 256 <= 64 && gemv2_fits(w)) return launch_gemv2(dm, w, x, y, yt, (hipStream_t)stream, epi);
   }
   if (kq && !xt && m >= 2 && m <= 16 && env_int("COMBS_GEMVD", 1))
     return launch_gemvd(dm, w, x, m, y, yt, (hipStream_t)stream, epi);

@@ -114,7 +114,7 @@ extern "C" __global__ void __launch_bounds__(256) cq_xsums_f16(const _Float16* x
 }
 
 #define GEMV1_KERNEL(NAME, FMT, YT, EPI)                                                \
-  extern "C" __global__ void __launch_bounds__(64 * gv1_waves<FMT>()) NAME(const Gv1Args a) { \
+  extern "C" __global__ void __launch_bounds__((64 * gv1_kernel_waves<FMT, EPI>())) NAME(const Gv1Args a) { \
     gemv1_body<FMT, YT, EPI>(a);                                                        \
   }
 #define GEMV1_FMT(fname, FMT)                          \

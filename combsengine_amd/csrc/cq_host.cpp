@@ -455,12 +455,14 @@ static cq_status launch_gemvd(DeviceModule* dm, const cq_weight* w, const void* 
   a.units = (int)(w->k / 256);
   a.epi = epi;
   // NT row tiles and nw waves per workgroup (at most one wave per
-  // superblock): 2 and 4 by default, the best measured pair on the Llama-3
-  // shapes at m = 4 / 16 (14.7 / 19.9 us for Q4_K 14336 x 4096).
-  int nt = env_int("COMBS_GVD_NT", 2);
+  // superblock), from a sweep of NT in {1, 2, 4}, nw in {2, 4, 8} and load
+  // depth 2..4 at the Llama-3-8B shapes (depth 2 best throughout): NT = 2
+  // (4 for Q6_K: lm_head m = 16 171 vs 204 us), nw = 4 (2 for m > 8 with
+  // long rows: Q4_K 4096 x 14336 m = 16 26.3 vs 29.7 us).
+  int nt = env_int("COMBS_GVD_NT", w->format == CQ_Q6_K ? 4 : 2);
   if (nt != 1 && nt != 2 && nt != 4) nt = 2;
   const long long wgs = (w->n + 16 * nt - 1) / (16 * nt);
-  int nw = env_int("COMBS_GVD_WAVES", 4);
+  int nw = env_int("COMBS_GVD_WAVES", m > 8 && a.units >= 32 ? 2 : 4);
   if (nw < 1 || nw > 8) nw = 4;
   if (nw > a.units) nw = a.units;
   if (wgs > 0x7fffffffLL) return fail(CQ_ERR_BAD_SHAPE, "grid too large (n=%lld)", (long long)w->n);

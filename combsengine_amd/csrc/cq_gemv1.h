@@ -547,18 +547,66 @@ __device__ __forceinline__ float gv3_superblock_q6k(const uint8_t* sb, const Gv3
   return d * __builtin_fmaf(16777216.0f, acc, -32.0f * cacc);
 }
 
+// Legacy units (eight 32-value blocks) against the lane's registers.  Q4_0
+// (gguf.rs:755-774): block b at byte 18 b, [d][16 qs]; value j = low nibble
+// of qs[j] at x[32 b + j], j + 16 = its high nibble; (q - 8) d, the -8 as
+// -8 * (block sum).  Q8_0 (gguf.rs:779-794): block b at 34 b, [d][32 qs];
+// q = qs[j] signed at x[32 b + j], fed as the byte q + 128 (a subnormal)
+// with -128 * (block sum).  Block fields are 2-byte aligned in LDS.
+template <int FMT>
+__device__ __forceinline__ float gv3_unit_legacy(const uint8_t* up, const Gv3XRegs& xr) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int blk = 0; blk < 8; blk++) {
+    float s0 = 0.0f, s1 = 0.0f;
+    if constexpr (FMT == CQ_Q4_0) {
+      const uint8_t* bp = up + 18 * blk;
+      const u4v q = ld_u128(bp + 2);
+      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+      float h0 = 0.0f, h1 = 0.0f;  // high nibbles, seen as 16 q
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t ws = w[i] >> 8;
+        const int m = 8 * blk + i;  // low nibbles: x[32 blk + 4 i ..]; high nibbles: 16 values on
+        s0 = fdot2u(w[i] & 0x000F000Fu, xr.xe[2 * m], s0);
+        s1 = fdot2u(ws & 0x000F000Fu, xr.xe[2 * m + 1], s1);
+        h0 = fdot2u(w[i] & 0x00F000F0u, xr.xe[2 * m + 8], h0);
+        h1 = fdot2u(ws & 0x00F000F0u, xr.xe[2 * m + 9], h1);
+      }
+      const float d = f16_bits_to_f32(ld_u16(bp));
+      const float sq = __builtin_fmaf(0.0625f, h0 + h1, s0 + s1);
+      acc = __builtin_fmaf(d, __builtin_fmaf(16777216.0f, sq, -8.0f * xr.su[blk]), acc);
+    } else {
+      const uint8_t* bp = up + 34 * blk;
+      u4v q[2];
+      q[0] = ld_u128(bp + 2);
+      q[1] = ld_u128(bp + 18);
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const uint32_t w = u4_word(q[i >> 2], i & 3) ^ 0x80808080u;
+        const int m = 8 * blk + i;
+        s0 = fdot2u(w & 0x00FF00FFu, xr.xe[2 * m], s0);
+        s1 = fdot2u((w >> 8) & 0x00FF00FFu, xr.xe[2 * m + 1], s1);
+      }
+      const float d = f16_bits_to_f32(ld_u16(bp));
+      acc = __builtin_fmaf(d, __builtin_fmaf(16777216.0f, s0 + s1, -128.0f * xr.su[blk]), acc);
+    }
+  }
+  return acc;
+}
+
 // Activation mode of cq_gemv1 per format: 1 = fp16 registers (Q4_K), 0 =
 // int8 three-part LDS staging.
 template <int FMT>
 constexpr int gv1_xmode() {
-  return FMT == CQ_Q4_K || FMT == CQ_Q6_K ? 1 : 0;
+  return FMT == CQ_Q4_K || FMT == CQ_Q6_K || FMT == CQ_Q4_0 || FMT == CQ_Q8_0 ? 1 : 0;
 }
 
 // Waves per workgroup: 8 (two per SIMD) where the register budget allows it
 // without spilling (Q4_K / Q5_K), else 4.
 template <int FMT>
 constexpr int gv1_waves() {
-  return FMT == CQ_Q4_K || FMT == CQ_Q5_K ? 8 : 4;
+  return FMT == CQ_Q4_K || FMT == CQ_Q5_K || FMT == CQ_Q4_0 ? 8 : 4;
 }
 
 // EPI = 0: no epilogue (a.epi empty), no loads at store time; EPI = 1: the
@@ -731,7 +779,8 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
       if (lane < lanes_used && rq < nrows) {
         const uint8_t* sbp = (const uint8_t*)(arr + wave * SP) + BB * lane;
         if constexpr (FMT == CQ_Q6_K) part = gv3_superblock_q6k(sbp, xregs);
-        else part = gv3_superblock_q4k((const u4v*)sbp, xregs);
+        else if constexpr (FMT == CQ_Q4_K) part = gv3_superblock_q4k((const u4v*)sbp, xregs);
+        else part = gv3_unit_legacy<FMT>(sbp, xregs);
       }
       task_store(part, tt);
     };
@@ -754,7 +803,7 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
     gv3_wait_vm<NI>();
     __syncthreads();
     xregs.load(myunit, x16p);
-    xregs.lane_sums<FMT == CQ_Q6_K ? 16 : 32>();
+    xregs.lane_sums<FMT == CQ_Q6_K ? 16 : 32>();  // (Q4_K / legacy: 32-value blocks)
     __syncthreads();  // the staged row (in gv_sb) fully read before any DMA into gv_sb
     for (int j = 0; j < n; j += 2, t += 2 * stride) {
       if (j + 1 < n) {

@@ -479,16 +479,16 @@ constexpr int kGv1MaxK = 16384;
 // Waves per cq_gemv1 workgroup (the kernels' launch bounds).
 static int gemv1_waves(int format, bool gated) {
   (void)gated;  // (the gated Q6_K kernel also runs 4 waves)
-  return format == CQ_Q4_K || format == CQ_Q5_K ? 8 : 4;
+  return format == CQ_Q4_K || format == CQ_Q5_K || format == CQ_Q4_0 ? 8 : 4;
 }
 // The quarter-superblock kernel (cq_gemv2) stages the row like cq_gemv1's
 // int8 path: K a multiple of 256, at most kGv1MaxK.
 static bool gemv2_fits(const cq_weight* w) { return w->k % 256 == 0 && w->k <= kGv1MaxK; }
 static bool gemv1_fits(const cq_weight* w) {
   if (!(gemv2_fits(w) && w->k / 256 <= 64)) return false;
-  // Q4_K / Q6_K run the LDS-DMA span path, whose 16-byte pieces must stay
-  // inside the weight: 16-byte aligned, size a multiple of 16
-  if (w->format == CQ_Q4_K || w->format == CQ_Q6_K)
+  // Q4_K / Q6_K / Q4_0 / Q8_0 run the LDS-DMA span path, whose 16-byte
+  // pieces must stay inside the weight: 16-byte aligned, size a multiple of 16
+  if (w->format == CQ_Q4_K || w->format == CQ_Q6_K || w->format == CQ_Q4_0 || w->format == CQ_Q8_0)
     return (reinterpret_cast<uintptr_t>(w->dev) & 15) == 0 && w->nbytes % 16 == 0;
   return true;
 }

@@ -487,9 +487,16 @@ static bool gemv2_fits(const cq_weight* w) { return w->k % 256 == 0 && w->k <= k
 static bool gemv1_fits(const cq_weight* w) {
   if (!(gemv2_fits(w) && w->k / 256 <= 64)) return false;
   // Q4_K / Q6_K / Q4_0 / Q8_0 run the LDS-DMA span path, whose 16-byte
-  // pieces must stay inside the weight: 16-byte aligned, size a multiple of 16
-  if (w->format == CQ_Q4_K || w->format == CQ_Q6_K || w->format == CQ_Q4_0 || w->format == CQ_Q8_0)
+  // pieces must stay inside the weight: it reads each task's span from its
+  // start in whole pieces, so the weight and every task span must start on
+  // a 16-byte boundary and the weight's size be a multiple of 16.  Task
+  // spans are R = 64 / units rows (1 from 64 units); 144- and 272-byte
+  // units keep them aligned, 210-byte Q6_K units need units * R % 8 == 0.
+  if (w->format == CQ_Q4_K || w->format == CQ_Q6_K || w->format == CQ_Q4_0 || w->format == CQ_Q8_0) {
+    const int64_t units = w->k / 256, rows = units >= 64 ? 1 : 64 / units;
+    if (w->format == CQ_Q6_K && (units * rows) % 8 != 0) return false;
     return (reinterpret_cast<uintptr_t>(w->dev) & 15) == 0 && w->nbytes % 16 == 0;
+  }
   return true;
 }
 // The one-launch gated gate/up: a task needs >= 2 rows of power-of-two units.

@@ -381,3 +381,21 @@ def test_gemv_batched_gaussian_llama_shape(cuda, fmt, m):
     finally:
         os.environ.pop("COMBS_GEMVD")
     O.assert_close(got, old, 1e-3, "mfma gemv")
+
+
+@pytest.mark.parametrize("fmt", [QuantFormat.Q4K, QuantFormat.Q6K, QuantFormat.Q4_0, QuantFormat.Q8_0])
+@pytest.mark.parametrize("n,k", [(300, 18944), (67, 16640), (40, 33024)])
+def test_gemv_single_row_long_k(cuda, fmt, n, k):
+    """m = 1 with K above the single-row kernels' 16384 (a Qwen2.5-7B down
+    projection is 18944 wide): served by the 16-row MFMA GEMV; fp32 and fp16
+    y, checked against the oracle and for bit-identical repeats."""
+    import torch
+    data = synth(fmt, n, k)
+    wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
+    w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
+    x = O.x_pattern(1, k, 13, 31, 15.0, 16.0).reshape(1, k)
+    print(f"long-k {fmt.name} n={n} k={k}", flush=True)
+    a = _run(w, x, torch.float16, torch.float32)
+    O.assert_close(a, O.ref_matmul(x, wd), rel_of(fmt), "y32")
+    assert np.array_equal(a.view(np.uint32), _run(w, x, torch.float16, torch.float32).view(np.uint32))
+    O.assert_close(_run(w, x, torch.float16, torch.float16), O.ref_matmul(x, wd), 1e-3, "y16")

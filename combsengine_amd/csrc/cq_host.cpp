@@ -455,14 +455,18 @@ static cq_status launch_gemvd(DeviceModule* dm, const cq_weight* w, const void* 
   a.units = (int)(w->k / 256);
   a.epi = epi;
   // NT row tiles and nw waves per workgroup (at most one wave per
-  // superblock), from a sweep of NT in {1, 2, 4}, nw in {2, 4, 8} and load
-  // depth 2..4 at the Llama-3-8B shapes (depth 2 best throughout): NT = 2
-  // (4 for Q6_K: lm_head m = 16 171 vs 204 us), nw = 4 (2 for m > 8 with
-  // long rows: Q4_K 4096 x 14336 m = 16 26.3 vs 29.7 us).
-  int nt = env_int("COMBS_GVD_NT", w->format == CQ_Q6_K ? 4 : 2);
+  // superblock), from sweeps of NT in {1, 2, 4} x nw in {2, 4, 8} (load
+  // depth 2..4: 2 best throughout) at the Llama-3-8B and Qwen2.5-7B shapes:
+  // NT = 1 below 8192 rows (Qwen2.5 down 3584 x 18944 Q6_K at m = 8: 30.0
+  // against 52.7 us with NT = 2), 4 for Q6_K from 32768 rows (lm_head
+  // m = 16: 171 against 204 us), else 2; nw = 4, or 2 for NT = 2 above
+  // m = 8, or 8 for NT = 1 up to m = 4 on rows of 32 or more superblocks
+  // (Q4_K 4096 x 14336 at m = 4: 18.6 against 24.0 us).
+  int nt = w->n < 8192 ? 1 : (w->format == CQ_Q6_K && w->n >= 32768) ? 4 : 2;
+  nt = env_int("COMBS_GVD_NT", nt);
   if (nt != 1 && nt != 2 && nt != 4) nt = 2;
   const long long wgs = (w->n + 16 * nt - 1) / (16 * nt);
-  int nw = env_int("COMBS_GVD_WAVES", m > 8 && a.units >= 32 ? 2 : 4);
+  int nw = env_int("COMBS_GVD_WAVES", nt == 2 && m > 8 ? 2 : nt == 1 && m <= 4 && a.units >= 32 ? 8 : 4);
   if (nw < 1 || nw > 8) nw = 4;
   if (nw > a.units) nw = a.units;
   if (wgs > 0x7fffffffLL) return fail(CQ_ERR_BAD_SHAPE, "grid too large (n=%lld)", (long long)w->n);

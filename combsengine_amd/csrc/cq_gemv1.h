@@ -547,6 +547,46 @@ __device__ __forceinline__ float gv3_superblock_q6k(const uint8_t* sb, const Gv3
   return d * __builtin_fmaf(16777216.0f, acc, -32.0f * cacc);
 }
 
+// Q5_K superblock (gguf.rs:929-961) against the lane's registers: as Q4_K,
+// plus the 5th bit of value (pair p, byte l) = bit 2p (low nibble) or
+// 2p + 1 (high nibble) of qh[l], moved to bit 4 of the low value's half
+// (q = nib | bit << 4) or bit 8 of the high one's (16 q = 16 nib | bit << 8),
+// both still fp16 subnormals.  Layout: header 16 bytes, qh 32, qs 128.
+__device__ __forceinline__ float gv3_superblock_q5k(const u4v* pc, const Gv3XRegs& xr) {
+  const u4v hd = pc[0];
+  float sc[8], mn[8];
+  gv1_scales(hd, sc, mn);
+  const float d = f16_bits_to_f32(hd.x), dmin = f16_bits_to_f32(hd.x >> 16);
+  float acc = 0.0f, macc = 0.0f;
+#pragma unroll
+  for (int p = 0; p < 4; p++) {
+    float lo0 = 0.0f, lo1 = 0.0f, hi0 = 0.0f, hi1 = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const u4v q = pc[3 + 2 * p + h], qh = pc[1 + h];
+      const uint32_t w[4] = {q.x, q.y, q.z, q.w}, hw[4] = {qh.x, qh.y, qh.z, qh.w};
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t ws = w[i] >> 8;
+        // bit 2p of qh bytes 0, 2 (1, 3) to bits 4, 20 and bit 2p + 1 to
+        // bits 8, 24 of the pair (0, 2) ((1, 3))
+        const uint32_t tl0 = p < 2 ? hw[i] << (4 - 2 * p) : hw[i] >> (2 * p - 4), tl1 = hw[i] >> (2 * p + 4);
+        const uint32_t th0 = hw[i] << (7 - 2 * p), th1 = hw[i] >> (2 * p + 1);
+        const int m = 16 * p + 4 * h + i;
+        lo0 = fdot2u((w[i] & 0x000F000Fu) | (tl0 & 0x00100010u), xr.xe[2 * m], lo0);
+        lo1 = fdot2u((ws & 0x000F000Fu) | (tl1 & 0x00100010u), xr.xe[2 * m + 1], lo1);
+        hi0 = fdot2u((w[i] & 0x00F000F0u) | (th0 & 0x01000100u), xr.xe[2 * m + 16], hi0);
+        hi1 = fdot2u((ws & 0x00F000F0u) | (th1 & 0x01000100u), xr.xe[2 * m + 17], hi1);
+      }
+    }
+    acc = __builtin_fmaf(sc[2 * p], lo0 + lo1, acc);
+    acc = __builtin_fmaf(sc[2 * p + 1] * 0.0625f, hi0 + hi1, acc);
+    macc = __builtin_fmaf(mn[2 * p], xr.su[2 * p], macc);
+    macc = __builtin_fmaf(mn[2 * p + 1], xr.su[2 * p + 1], macc);
+  }
+  return d * (acc * 16777216.0f) - dmin * macc;
+}
+
 // Legacy units (eight 32-value blocks) against the lane's registers.  Q4_0
 // (gguf.rs:755-774): block b at byte 18 b, [d][16 qs]; value j = low nibble
 // of qs[j] at x[32 b + j], j + 16 = its high nibble; (q - 8) d, the -8 as
@@ -599,14 +639,14 @@ __device__ __forceinline__ float gv3_unit_legacy(const uint8_t* up, const Gv3XRe
 // int8 three-part LDS staging.
 template <int FMT>
 constexpr int gv1_xmode() {
-  return FMT == CQ_Q4_K || FMT == CQ_Q6_K || FMT == CQ_Q4_0 || FMT == CQ_Q8_0 ? 1 : 0;
+  return FMT == CQ_Q4_K || FMT == CQ_Q5_K || FMT == CQ_Q6_K || FMT == CQ_Q4_0 || FMT == CQ_Q8_0 ? 1 : 0;
 }
 
 // Waves per workgroup: 8 (two per SIMD) where the register budget allows it
 // without spilling (Q4_K / Q5_K), else 4.
 template <int FMT>
 constexpr int gv1_waves() {
-  return FMT == CQ_Q4_K || FMT == CQ_Q5_K || FMT == CQ_Q4_0 ? 8 : 4;
+  return FMT == CQ_Q4_K || FMT == CQ_Q4_0 ? 8 : 4;
 }
 
 // EPI = 0: no epilogue (a.epi empty), no loads at store time; EPI = 1: the
@@ -780,6 +820,7 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
         const uint8_t* sbp = (const uint8_t*)(arr + wave * SP) + BB * lane;
         if constexpr (FMT == CQ_Q6_K) part = gv3_superblock_q6k(sbp, xregs);
         else if constexpr (FMT == CQ_Q4_K) part = gv3_superblock_q4k((const u4v*)sbp, xregs);
+        else if constexpr (FMT == CQ_Q5_K) part = gv3_superblock_q5k((const u4v*)sbp, xregs);
         else part = gv3_unit_legacy<FMT>(sbp, xregs);
       }
       task_store(part, tt);

@@ -483,20 +483,21 @@ constexpr int kGv1MaxK = 16384;
 // Waves per cq_gemv1 workgroup (the kernels' launch bounds).
 static int gemv1_waves(int format, bool gated) {
   (void)gated;  // (the gated Q6_K kernel also runs 4 waves)
-  return format == CQ_Q4_K || format == CQ_Q5_K || format == CQ_Q4_0 ? 8 : 4;
+  return format == CQ_Q4_K || format == CQ_Q4_0 ? 8 : 4;
 }
 // The quarter-superblock kernel (cq_gemv2) stages the row like cq_gemv1's
 // int8 path: K a multiple of 256, at most kGv1MaxK.
 static bool gemv2_fits(const cq_weight* w) { return w->k % 256 == 0 && w->k <= kGv1MaxK; }
 static bool gemv1_fits(const cq_weight* w) {
   if (!(gemv2_fits(w) && w->k / 256 <= 64)) return false;
-  // Q4_K / Q6_K / Q4_0 / Q8_0 run the LDS-DMA span path, whose 16-byte
+  // Q4_K / Q5_K / Q6_K / Q4_0 / Q8_0 run the LDS-DMA span path, whose 16-byte
   // pieces must stay inside the weight: it reads each task's span from its
   // start in whole pieces, so the weight and every task span must start on
   // a 16-byte boundary and the weight's size be a multiple of 16.  Task
   // spans are R = 64 / units rows (1 from 64 units); 144- and 272-byte
   // units keep them aligned, 210-byte Q6_K units need units * R % 8 == 0.
-  if (w->format == CQ_Q4_K || w->format == CQ_Q6_K || w->format == CQ_Q4_0 || w->format == CQ_Q8_0) {
+  if (w->format == CQ_Q4_K || w->format == CQ_Q5_K || w->format == CQ_Q6_K || w->format == CQ_Q4_0 ||
+      w->format == CQ_Q8_0) {
     const int64_t units = w->k / 256, rows = units >= 64 ? 1 : 64 / units;
     if (w->format == CQ_Q6_K && (units * rows) % 8 != 0) return false;
     return (reinterpret_cast<uintptr_t>(w->dev) & 15) == 0 && w->nbytes % 16 == 0;

@@ -180,6 +180,7 @@ struct DeviceModule {
   hipFunction_t xsums = nullptr;
   hipFunction_t reduce[2] = {};       // split-K epilogue [y f16]
   hipFunction_t gemv1[kNumFormats][2][3] = {};  // [format][y f16][epilogue: none, general, gated]
+  hipFunction_t gemv1_i8[kNumFormats][2][2] = {};  // int8 variant of Q4_K / Q4_0 / Q8_0 [format][y f16][epilogue]
   hipFunction_t gemv2[kNumFormats][2][2] = {};  // K-quants only     // [format][y f16]
   hipFunction_t gemvd[kNumFormats][3][2] = {};  // K-quants only: [format][NT 1, 2, 4][y f16]
   int cus = 0;                        // compute units of the device
@@ -246,6 +247,14 @@ void load_module(DeviceModule& d, int dev) {
         if (hipModuleGetFunction(&d.gemv1[fi][yt][ep], d.mod, name) != hipSuccess) {
           d.err = std::string("missing kernel ") + name;
           return;
+        }
+        const int f = kFormats[fi];
+        if (ep < 2 && (f == CQ_Q4_K || f == CQ_Q4_0 || f == CQ_Q8_0)) {
+          snprintf(name, sizeof name, "cq_gemv1_%s_y%s%s_i8", fmt_name(f), yt ? "f16" : "f32", ep ? "_epi" : "");
+          if (hipModuleGetFunction(&d.gemv1_i8[fi][yt][ep], d.mod, name) != hipSuccess) {
+            d.err = std::string("missing kernel ") + name;
+            return;
+          }
         }
         if (block_values(kFormats[fi]) != 256) continue;
         if (ep == 0)
@@ -530,14 +539,21 @@ static cq_status launch_gemv1(DeviceModule* dm, const cq_weight* w, const void* 
   a.span = env_int("COMBS_GEMV1_SPAN", 1);
   a.wave_major = env_int("COMBS_GEMV1_WAVE_MAJOR", 0);
   a.epi = epi;
-  const int nw = gemv1_waves(w->format, up != nullptr);
-  const int wgs = (a.tasks + nw - 1) / nw;
+  const int ep = up ? 2 : (epi.bias || epi.aux) ? 1 : 0;
+  // Small weights (no more tasks than the register path's grid has waves):
+  // the int8 path's set-up is cheaper than loading the activation registers.
+  hipFunction_t k = dm->gemv1[fi][yt][ep];
+  int nw = gemv1_waves(w->format, up != nullptr);
   int cap = env_int("COMBS_GEMV1_GRID", dm->cus);
   if (cap < 1) cap = 1;
+  if (ep < 2 && dm->gemv1_i8[fi][yt][ep] && a.tasks <= (int64_t)cap * nw && env_int("COMBS_GEMV1_I8", 1)) {
+    k = dm->gemv1_i8[fi][yt][ep];
+    nw = w->format == CQ_Q4_K ? 8 : 4;  // the _i8 kernels' waves
+  }
+  const int wgs = (a.tasks + nw - 1) / nw;
   const int grid = wgs < cap ? wgs : cap;
   void* params[] = {&a};
-  const int ep = up ? 2 : (epi.bias || epi.aux) ? 1 : 0;
-  HIP_TRY(hipModuleLaunchKernel(dm->gemv1[fi][yt][ep], (unsigned)grid, 1, 1, 64 * nw, 1, 1, 0, s, params, nullptr));
+  HIP_TRY(hipModuleLaunchKernel(k, (unsigned)grid, 1, 1, 64 * nw, 1, 1, 0, s, params, nullptr));
   return CQ_OK;
 }
 

@@ -790,6 +790,12 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
     __shared__ __attribute__((aligned(16))) u4v gv_sa[NW * SP];
     __shared__ __attribute__((aligned(16))) u4v gv_sb[NW * SP];
     static_assert(NW * SP * 16 >= GV1_XMAX / 256 * 528, "the staged row fits in gv_sb");
+    // Rows of at most XU units are staged in LDS left over beside the slices
+    // (gv_sx) instead of in gv_sb, so both of a wave's first two tasks go out
+    // before the staging.
+    constexpr int XU = (163840 - 2 * NW * SP * 16) / 528 < 64 ? (163840 - 2 * NW * SP * 16) / 528 : 64;
+    __shared__ __attribute__((aligned(16))) u4v gv_sx[XU * 33];
+    const bool xsep = a.K <= 256 * XU;
     const int n = t < a.tasks ? (a.tasks - 1 - t) / stride + 1 : 0;
     auto dma_task = [&](u4v* arr, int tt) {
       const uint8_t *b0, *b1;
@@ -831,7 +837,7 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
     // unit in one LDS bank.  A unit is one half-wave instruction (32 lanes x
     // 16 bytes); waves take unit pairs in turn.  These DMAs are the older
     // ones in the counter.
-    _Float16* x16p = (_Float16*)gv_sb;
+    _Float16* x16p = (_Float16*)(xsep ? gv_sx : gv_sb);
     {
       const int nunits = a.K / 256;
       for (int u0 = 2 * wave; u0 < nunits; u0 += 2 * NW) {
@@ -841,6 +847,33 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
       }
     }
     dma_task(gv_sa, min(t, a.tasks - 1));
+    if (xsep) {
+      // Row in gv_sx: the second task goes out at once.
+      if (n > 1) {
+        dma_task(gv_sb, t + stride);
+        gv3_wait_vm<2 * NI>();
+      } else {
+        gv3_wait_vm<NI>();
+      }
+      __syncthreads();
+      xregs.load(myunit, x16p);
+      xregs.lane_sums<FMT == CQ_Q6_K ? 16 : 32>();
+      // Invariant at the top: tasks j (gv_sa) and j + 1 (gv_sb, if any) issued.
+      for (int j = 0; j < n; j += 2, t += 2 * stride) {
+        if (j + 1 < n) gv3_wait_vm<NI>();
+        else gv3_wait_vm<0>();
+        compute(gv_sa, t);
+        if (j + 1 >= n) break;
+        if (j + 2 < n) {
+          dma_task(gv_sa, t + 2 * stride);
+          gv3_wait_vm<NI>();
+        } else {
+          gv3_wait_vm<0>();
+        }
+        compute(gv_sb, t + stride);
+        if (j + 3 < n) dma_task(gv_sb, t + 3 * stride);
+      }
+    } else {
     gv3_wait_vm<NI>();
     __syncthreads();
     xregs.load(myunit, x16p);
@@ -865,6 +898,7 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
         gv3_wait_vm<0>();
       }
       compute(gv_sb, t + stride);
+    }
     }
     // no LDS DMA may still be landing when the workgroup's LDS is handed on
     // (a wave without tasks still loaded one into its first slice)

@@ -625,8 +625,10 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
   if (nt != 1 && nt != 2) nt = (w->n + 16 * nw - 1) / (16 * nw) * mblk * 2 >= slots ? 2 : 1;  // NT = 2 while it fills half the slots
   const long long gx = (w->n + 16 * nw * nt - 1) / (16 * nw * nt);
   if (gx > 0x7fffffffLL || mblk > 65535) return fail(CQ_ERR_BAD_SHAPE, "grid too large");
-  // Split K when the tiles leave compute units idle (each slice keeps >= 4
-  // superblocks); COMBS_GEMM2_SPLIT forces the slice count.
+  // Split K when the tiles leave compute units idle (each slice keeps >= 3
+  // superblocks: at N = 512, K = 3584, m = 512 four slices of 3-4 measured
+  // 27 / 23 us (Q4_K / Q6_K) against 31 / 32 us for two; slices of 2 were
+  // slower at N = 1024, K = 4096); COMBS_GEMM2_SPLIT forces the slice count.
   // Not while the stream is being captured into a graph: split-K inside a
   // captured graph has not been verified on the GPU, so captured launches
   // take the unsplit path.
@@ -635,7 +637,7 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
   int splits = cs == hipStreamCaptureStatusNone ? env_int("COMBS_GEMM2_SPLIT", 0) : 1;
   if (splits < 1) {
     splits = 1;
-    while (gx * mblk * splits * 2 <= slots && a.units / (splits * 2) >= 4) splits *= 2;
+    while (gx * mblk * splits * 2 <= slots && a.units / (splits * 2) >= 3) splits *= 2;
   }
   if (splits > a.units) splits = a.units;
   a.usplit = (a.units + splits - 1) / splits;

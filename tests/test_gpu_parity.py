@@ -265,12 +265,13 @@ def test_gemm_split_k(cuda, monkeypatch, fmt, split, m):
 
 
 @pytest.mark.parametrize("fmt", KQ)
-def test_gemm_split_k_auto_down_projection(cuda, fmt):
-    """A down-projection-like shape (few weight rows, long K) takes the
-    automatic split; checked against float64 torch on the GPU dequant."""
+@pytest.mark.parametrize("n,k,m", [(512, 7168, 64), (512, 3584, 512)])
+def test_gemm_split_k_auto_down_projection(cuda, fmt, n, k, m):
+    """Shapes with few weight rows take the automatic split (512 x 3584 at
+    m = 512: four slices of 4, 4, 4, 2 superblocks); checked against float64
+    torch on the GPU dequant."""
     import torch
     rng = np.random.default_rng(11 + int(fmt))
-    n, k, m = 512, 7168, 64
     data = quantize(fmt, rng.normal(0, 0.02, (n, k)).astype(np.float32))
     w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
     wd = torch.from_numpy(dequantize_gpu(fmt, data).reshape(n, k)).cuda().double()

@@ -540,18 +540,32 @@ static cq_status launch_gemv1(DeviceModule* dm, const cq_weight* w, const void* 
   a.wave_major = env_int("COMBS_GEMV1_WAVE_MAJOR", 0);
   a.epi = epi;
   const int ep = up ? 2 : (epi.bias || epi.aux) ? 1 : 0;
-  // Small weights (no more tasks than the register path's grid has waves):
-  // the int8 path's set-up is cheaper than loading the activation registers.
+  // Weights with fewer workgroups of tasks than compute units spread their
+  // tasks over every compute unit, wave-major (task t on wave t / grid of
+  // workgroup t % grid): workgroup-major packing left most compute units
+  // idle (Q4_K 1024 x 4096: 5.9 -> 4.6 us; 4096 x 4096: 6.2 -> 5.6 us).
+  // COMBS_GEMV1_SPREAD=0 turns this off.  The int8 path's cheaper set-up
+  // pays for Q4_0 / Q8_0 weights with more tasks than workgroups (4096 x
+  // 4096: 5.5 / 7.2 against 5.8 / 7.5 us); with at most one task per
+  // workgroup, and for Q4_K, the register path is faster.  COMBS_GEMV1_I8:
+  // 0 never, 2 whenever the weight is small.
   hipFunction_t k = dm->gemv1[fi][yt][ep];
   int nw = gemv1_waves(w->format, up != nullptr);
   int cap = env_int("COMBS_GEMV1_GRID", dm->cus);
   if (cap < 1) cap = 1;
-  if (ep < 2 && dm->gemv1_i8[fi][yt][ep] && a.tasks <= (int64_t)cap * nw && env_int("COMBS_GEMV1_I8", 1)) {
+  const int i8 = env_int("COMBS_GEMV1_I8", 1);
+  const int i8w = w->format == CQ_Q4_K ? 8 : 4;  // the _i8 kernels' waves
+  if (ep < 2 && dm->gemv1_i8[fi][yt][ep] && a.tasks <= (int64_t)cap * i8w &&
+      (i8 == 2 || (i8 == 1 && w->format != CQ_Q4_K && a.tasks > cap))) {
     k = dm->gemv1_i8[fi][yt][ep];
-    nw = w->format == CQ_Q4_K ? 8 : 4;  // the _i8 kernels' waves
+    nw = i8w;
   }
   const int wgs = (a.tasks + nw - 1) / nw;
-  const int grid = wgs < cap ? wgs : cap;
+  int grid = wgs < cap ? wgs : cap;
+  if (env_int("COMBS_GEMV1_SPREAD", 1) && wgs < cap) {
+    a.wave_major = 1;
+    grid = a.tasks < cap ? a.tasks : cap;
+  }
   void* params[] = {&a};
   HIP_TRY(hipModuleLaunchKernel(k, (unsigned)grid, 1, 1, 64 * nw, 1, 1, 0, s, params, nullptr));
   return CQ_OK;

@@ -190,7 +190,8 @@ ALL_FMTS = FMTS + [QuantFormat.Q4_1, QuantFormat.Q5_1]
 @pytest.mark.parametrize("n,k", [(300, 4096), (257, 256), (130, 8192), (45, 1024), (97, 3584)])
 @pytest.mark.parametrize("fused", ["1", "0"])
 @pytest.mark.parametrize("y_dt", ["f32", "f16"])
-def test_gate_up_single_row_one_launch(cuda, monkeypatch, fmt, n, k, fused, y_dt):
+@pytest.mark.parametrize("spread", ["1", "0"])
+def test_gate_up_single_row_one_launch(cuda, monkeypatch, fmt, n, k, fused, y_dt, spread):
     """m = 1, fp16 x, gate and up of one format: the one-launch kernel (both
     weights against one activation staging, R/2 gate and R/2 up rows per
     task, ragged last task) for K/256 a power of two up to 32; K = 3584
@@ -198,6 +199,7 @@ def test_gate_up_single_row_one_launch(cuda, monkeypatch, fmt, n, k, fused, y_dt
     kernel multiplies the fp32 up product (no fp16 rounding in between)."""
     import torch
     monkeypatch.setenv("COMBS_GATEUP_FUSED", fused)
+    monkeypatch.setenv("COMBS_GEMV1_SPREAD", spread)  # tasks wave-major over the grid, or packed
     gd, gw = _weight(fmt, n, k, 90 + int(fmt))
     ud, uw = _weight(fmt, n, k, 95 + int(fmt))
     x = _x(1, k, 96)

@@ -163,21 +163,25 @@ KQ = [QuantFormat.Q4K, QuantFormat.Q5K, QuantFormat.Q6K]
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("n,k", [(300, 4096), (35, 512), (97, 3584), (50, 5120), (70, 14336), (130, 16384), (1, 256),
                                  (2053, 1024), (3000, 768), (9, 4352)])
-@pytest.mark.parametrize("kernel", ["gemv2", "gemv1", "gemv1reg", "mfma"])
+@pytest.mark.parametrize("kernel", ["gemv2", "gemv1", "gemv1reg", "gemv1i8", "gemv1packed", "mfma"])
 def test_gemv_single_row(cuda, monkeypatch, fmt, n, k, kernel):
     """m = 1 fp16 decode through each single-row kernel: the streaming
     quarter-superblock kernel (gemv2, K-quants: steps of 16 superblocks, R =
     16/units rows per step for units 1/2/4/8, several steps per row above 16,
     ragged row ranges per wave), the whole-superblock kernel (gemv1: wave
     tasks of 64/units rows, units from 1 to 64; by default small weights of
-    Q4_K / Q4_0 / Q8_0 take its int8 path, gemv1reg forces the fp16-register
-    path) and the 16-row MFMA kernel; fp32 and fp16 outputs."""
+    Q4_0 / Q8_0 with more tasks than workgroups take its int8 path, gemv1reg
+    forces the fp16-register path, gemv1i8 the int8 path for Q4_K / Q4_0 /
+    Q8_0; small weights spread their tasks wave-major over the grid,
+    gemv1packed packs them workgroup-major) and the 16-row MFMA kernel; fp32
+    and fp16 outputs."""
     import torch
     if kernel == "gemv2" and fmt in LEGACY:
         pytest.skip("gemv2 serves the K-quants")
     monkeypatch.setenv("COMBS_GEMV1", "0" if kernel == "mfma" else "1")
     monkeypatch.setenv("COMBS_GEMV2", "2" if kernel == "gemv2" else "0")
-    monkeypatch.setenv("COMBS_GEMV1_I8", "0" if kernel == "gemv1reg" else "1")
+    monkeypatch.setenv("COMBS_GEMV1_I8", {"gemv1reg": "0", "gemv1i8": "2"}.get(kernel, "1"))
+    monkeypatch.setenv("COMBS_GEMV1_SPREAD", "0" if kernel == "gemv1packed" else "1")
     data = synth(fmt, n, k)
     wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
     w = QuantWeight.from_gguf_bytes(fmt, data, n, k)

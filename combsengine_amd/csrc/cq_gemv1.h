@@ -790,12 +790,6 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
     __shared__ __attribute__((aligned(16))) u4v gv_sa[NW * SP];
     __shared__ __attribute__((aligned(16))) u4v gv_sb[NW * SP];
     static_assert(NW * SP * 16 >= GV1_XMAX / 256 * 528, "the staged row fits in gv_sb");
-    // Rows of at most XU units are staged in LDS left over beside the slices
-    // (gv_sx) instead of in gv_sb, so both of a wave's first two tasks go out
-    // before the staging.
-    constexpr int XU = (163840 - 2 * NW * SP * 16) / 528 < 64 ? (163840 - 2 * NW * SP * 16) / 528 : 64;
-    __shared__ __attribute__((aligned(16))) u4v gv_sx[XU * 33];
-    const bool xsep = a.K <= 256 * XU;
     const int n = t < a.tasks ? (a.tasks - 1 - t) / stride + 1 : 0;
     auto dma_task = [&](u4v* arr, int tt) {
       const uint8_t *b0, *b1;
@@ -837,7 +831,7 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
     // unit in one LDS bank.  A unit is one half-wave instruction (32 lanes x
     // 16 bytes); waves take unit pairs in turn.  These DMAs are the older
     // ones in the counter.
-    _Float16* x16p = (_Float16*)(xsep ? gv_sx : gv_sb);
+    _Float16* x16p = (_Float16*)gv_sb;
     {
       const int nunits = a.K / 256;
       for (int u0 = 2 * wave; u0 < nunits; u0 += 2 * NW) {
@@ -847,33 +841,6 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
       }
     }
     dma_task(gv_sa, min(t, a.tasks - 1));
-    if (xsep) {
-      // Row in gv_sx: the second task goes out at once.
-      if (n > 1) {
-        dma_task(gv_sb, t + stride);
-        gv3_wait_vm<2 * NI>();
-      } else {
-        gv3_wait_vm<NI>();
-      }
-      __syncthreads();
-      xregs.load(myunit, x16p);
-      xregs.lane_sums<FMT == CQ_Q6_K ? 16 : 32>();
-      // Invariant at the top: tasks j (gv_sa) and j + 1 (gv_sb, if any) issued.
-      for (int j = 0; j < n; j += 2, t += 2 * stride) {
-        if (j + 1 < n) gv3_wait_vm<NI>();
-        else gv3_wait_vm<0>();
-        compute(gv_sa, t);
-        if (j + 1 >= n) break;
-        if (j + 2 < n) {
-          dma_task(gv_sa, t + 2 * stride);
-          gv3_wait_vm<NI>();
-        } else {
-          gv3_wait_vm<0>();
-        }
-        compute(gv_sb, t + stride);
-        if (j + 3 < n) dma_task(gv_sb, t + 3 * stride);
-      }
-    } else {
     gv3_wait_vm<NI>();
     __syncthreads();
     xregs.load(myunit, x16p);
@@ -898,7 +865,6 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
         gv3_wait_vm<0>();
       }
       compute(gv_sb, t + stride);
-    }
     }
     // no LDS DMA may still be landing when the workgroup's LDS is handed on
     // (a wave without tasks still loaded one into its first slice)
@@ -945,4 +911,116 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
     }
   }
   }
+}
+
+// Single-row decode for rows longer than one wave's 64 units (65 to 128
+// units, 106 for Q6_K: K from 16640 to 32768, the register-path formats
+// other than Q8_0).  A workgroup is two wave pairs; in a pair, wave 2g + p keeps
+// the activations of the row's half p (units p * ceil(units / 2) ..) in
+// registers and takes that half of every row the pair serves, by LDS DMA
+// of its byte range (from the 16-byte boundary at or below its start:
+// 210-byte Q6_K units leave half spans at any even offset, which the
+// superblock reads accept).  Both halves' sums meet in LDS, one barrier per
+// row; the pair's first wave adds them in a fixed order and stores.
+constexpr int GV1K_WAVES = 4;
+template <int FMT>
+constexpr int gv1k_xunits() {
+  // units of the staged activation row that fit beside the two slices
+  constexpr int sp = 64 * gv1_unit_bytes<FMT>() / 16 + 1;
+  constexpr int left = (163840 - 2 * GV1K_WAVES * sp * 16 - 64) / 528;
+  return left < 128 ? left : 128;
+}
+template <int FMT, int YT, int EPI>
+__device__ __forceinline__ void gemv1k_body(const Gv1Args& a) {
+  constexpr int NW = GV1K_WAVES, G = NW / 2;
+  constexpr int BB = gv1_unit_bytes<FMT>();
+  constexpr int SP = 64 * BB / 16 + 1;  // pieces per slice: 64 units and a start offset
+  constexpr int NI = (SP + 63) / 64;
+  constexpr int XU = gv1k_xunits<FMT>();
+  __shared__ __attribute__((aligned(16))) u4v gk_sa[NW * SP];
+  __shared__ __attribute__((aligned(16))) u4v gk_sb[NW * SP];
+  __shared__ __attribute__((aligned(16))) u4v gk_x[XU * 33];
+  __shared__ float gk_red[2][NW];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int p = wave & 1, g = wave >> 1;
+  const int upart = (a.units + 1) >> 1;
+  const int u0 = p * upart, cnt = min(upart, a.units - u0);
+  const int rstride = (int)gridDim.x * G, rbase = (int)blockIdx.x * G;
+  // rows served: rbase + g + i * rstride; every wave of the workgroup runs
+  // the same n iterations (group 0's count), so the barriers match
+  const int n = rbase < a.N ? (a.N - 1 - rbase) / rstride + 1 : 0;
+  if (n == 0) return;
+  auto start_of = [&](int i) {
+    const int r = min(rbase + g + i * rstride, a.N - 1);
+    return (size_t)r * (size_t)a.row_bytes + (size_t)u0 * BB;
+  };
+  auto dma_task = [&](u4v* arr, int i) {
+    const size_t st = start_of(i);
+    const uint8_t* b = a.w + (st & ~(size_t)15);
+    const int lim = (int)(((st & 15) + (size_t)cnt * BB + 15) >> 4);  // pieces that hold the half
+    u4v* dst = arr + wave * SP;
+#pragma unroll
+    for (int k = 0; k < NI; k++) {
+      const int q = 64 * k + lane;
+      if (SP % 64 == 0 || k + 1 < NI || q < SP) gv3_dma16(b + 16 * min(q, lim - 1), gv3_lds_addr(dst + 64 * k));
+    }
+  };
+  Gv3XRegs xregs;
+  auto compute = [&](const u4v* arr, int i) {
+    const int r = rbase + g + i * rstride;
+    float part = 0.0f;
+    if (lane < cnt) {
+      const uint8_t* sbp = (const uint8_t*)(arr + wave * SP) + (start_of(i) & 15) + BB * lane;
+      if constexpr (FMT == CQ_Q6_K) part = gv3_superblock_q6k(sbp, xregs);
+      else if constexpr (FMT == CQ_Q4_K) part = gv3_superblock_q4k((const u4v*)sbp, xregs);
+      else if constexpr (FMT == CQ_Q5_K) part = gv3_superblock_q5k((const u4v*)sbp, xregs);
+      else part = gv3_unit_legacy<FMT>(sbp, xregs);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+    if (lane == 0) gk_red[i & 1][wave] = part;
+    __syncthreads();
+    if (p == 0 && lane == 0 && r < a.N) {
+      const float v = gk_red[i & 1][wave] + gk_red[i & 1][wave + 1];
+      if constexpr (EPI == 1) cq_store<YT>(a.y, a.epi, v, r, r);
+      else cq_store_raw<YT>(a.y, v, r);
+    }
+  };
+  // activation row -> gk_x (unit u at 528 u bytes), as in cq_gemv1
+  _Float16* x16p = (_Float16*)gk_x;
+  {
+    const int nunits = a.K / 256;
+    for (int v0 = 2 * wave; v0 < nunits; v0 += 2 * NW) {
+      if (lane < 32) gv3_dma16(a.x + 256 * v0 + 8 * lane, gv3_lds_addr(x16p + 264 * v0));
+      if (lane >= 32 && v0 + 1 < nunits)
+        gv3_dma16(a.x + 256 * (v0 + 1) + 8 * (lane - 32), gv3_lds_addr(x16p + 264 * (v0 + 1)) - 512);
+    }
+  }
+  dma_task(gk_sa, 0);
+  if (n > 1) {
+    dma_task(gk_sb, 1);
+    gv3_wait_vm<2 * NI>();
+  } else {
+    gv3_wait_vm<NI>();
+  }
+  __syncthreads();
+  xregs.load(u0 + min(lane, cnt - 1), x16p);
+  xregs.lane_sums<FMT == CQ_Q6_K ? 16 : 32>();
+  // Invariant at the top: rows i (gk_sa) and i + 1 (gk_sb, if any) issued.
+  for (int i = 0; i < n; i += 2) {
+    if (i + 1 < n) gv3_wait_vm<NI>();
+    else gv3_wait_vm<0>();
+    compute(gk_sa, i);
+    if (i + 1 >= n) break;
+    if (i + 2 < n) {
+      dma_task(gk_sa, i + 2);
+      gv3_wait_vm<NI>();
+    } else {
+      gv3_wait_vm<0>();
+    }
+    compute(gk_sb, i + 1);
+    if (i + 3 < n) dma_task(gk_sb, i + 3);
+  }
+  gv3_wait_vm<0>();
 }

@@ -180,7 +180,8 @@ struct DeviceModule {
   hipFunction_t xsums = nullptr;
   hipFunction_t reduce[2] = {};       // split-K epilogue [y f16]
   hipFunction_t gemv1[kNumFormats][2][3] = {};  // [format][y f16][epilogue: none, general, gated]
-  hipFunction_t gemv1_i8[kNumFormats][2][2] = {};  // int8 variant of Q4_K / Q4_0 / Q8_0 [format][y f16][epilogue]
+  hipFunction_t gemv1_i8[kNumFormats][2][2] = {};
+  hipFunction_t gemv1k[kNumFormats][2][2] = {};   // rows of 65-128 units, Q4_K / Q5_K / Q6_K / Q4_0 [format][y f16][epilogue]
   hipFunction_t gemv2[kNumFormats][2][2] = {};  // K-quants only     // [format][y f16]
   hipFunction_t gemvd[kNumFormats][3][2] = {};  // K-quants only: [format][NT 1, 2, 4][y f16]
   int cus = 0;                        // compute units of the device
@@ -252,6 +253,13 @@ void load_module(DeviceModule& d, int dev) {
         if (ep < 2 && (f == CQ_Q4_K || f == CQ_Q4_0 || f == CQ_Q8_0)) {
           snprintf(name, sizeof name, "cq_gemv1_%s_y%s%s_i8", fmt_name(f), yt ? "f16" : "f32", ep ? "_epi" : "");
           if (hipModuleGetFunction(&d.gemv1_i8[fi][yt][ep], d.mod, name) != hipSuccess) {
+            d.err = std::string("missing kernel ") + name;
+            return;
+          }
+        }
+        if (ep < 2 && (f == CQ_Q4_K || f == CQ_Q5_K || f == CQ_Q6_K || f == CQ_Q4_0)) {
+          snprintf(name, sizeof name, "cq_gemv1k_%s_y%s%s", fmt_name(f), yt ? "f16" : "f32", ep ? "_epi" : "");
+          if (hipModuleGetFunction(&d.gemv1k[fi][yt][ep], d.mod, name) != hipSuccess) {
             d.err = std::string("missing kernel ") + name;
             return;
           }
@@ -513,6 +521,46 @@ static bool gemv1_fits(const cq_weight* w) {
   }
   return true;
 }
+// Rows of 65 to 128 units (K 16640 to 32768) on cq_gemv1k_*: Q4_K / Q5_K /
+// Q6_K / Q4_0, the weight 16-byte aligned and a multiple of 16 bytes (its
+// DMA pieces run from the 16-byte boundary at or below each half row), the
+// staged activation row within the kernel's LDS (Q6_K: 106 units).
+static int gemv1k_max_units(int format) {
+  switch (format) {
+    case CQ_Q4_K: case CQ_Q4_0: return 128;
+    case CQ_Q5_K: return 128;
+    case CQ_Q6_K: return 106;
+    default: return 0;
+  }
+}
+static bool gemv1k_fits(const cq_weight* w) {
+  const int64_t u = w->k / 256;
+  return w->k % 256 == 0 && u > 64 && u <= gemv1k_max_units(w->format) &&
+         (reinterpret_cast<uintptr_t>(w->dev) & 15) == 0 && w->nbytes % 16 == 0;
+}
+static cq_status launch_gemv1k(DeviceModule* dm, const cq_weight* w, const void* x, void* y, int yt, hipStream_t s,
+                               const CqEpi& epi) {
+  const int fi = fmt_index(w->format);
+  Gv1Args a{};
+  a.w = w->dev;
+  a.w2 = nullptr;
+  a.x = x;
+  a.y = y;
+  a.row_bytes = (long long)(w->nbytes / (size_t)w->n);
+  a.N = (int)w->n;
+  a.K = (int)w->k;
+  a.units = (int)(w->k / 256);
+  a.rows = 1;
+  a.tasks = a.N;
+  a.epi = epi;
+  const int ep = (epi.bias || epi.aux) ? 1 : 0;
+  constexpr int kPairs = 2;  // wave pairs per workgroup (the kernels' launch bounds: 4 waves)
+  const int64_t need = (w->n + kPairs - 1) / kPairs;
+  const int grid = (int)(need < dm->cus ? need : dm->cus);
+  void* params[] = {&a};
+  HIP_TRY(hipModuleLaunchKernel(dm->gemv1k[fi][yt][ep], (unsigned)grid, 1, 1, 64 * 4, 1, 1, 0, s, params, nullptr));
+  return CQ_OK;
+}
 // The one-launch gated gate/up: a task needs >= 2 rows of power-of-two units.
 static bool gemv1_gated_fits(const cq_weight* w) {
   const int64_t u = w->k / 256;
@@ -743,6 +791,7 @@ static cq_status matmul_impl(const cq_weight* w, const void* x, int x_dtype, int
     if (kq && (g2 == 2 || (g2 == 1 && w->format == CQ_Q6_K)) && gemv2_fits(w))
       return launch_gemv2(dm, w, x, y, yt, (hipStream_t)stream, epi);
     if (gemv1_fits(w)) return launch_gemv1(dm, w, x, y, yt, (hipStream_t)stream, epi);
+    if (gemv1k_fits(w) && env_int("COMBS_GEMV1K", 1)) return launch_gemv1k(dm, w, x, y, yt, (hipStream_t)stream, epi);
     if (kq && w->k / 256 <= 64 && gemv2_fits(w)) return launch_gemv2(dm, w, x, y, yt, (hipStream_t)stream, epi);
   }
   if (kq && !xt && m >= 2 && m <= 16 && env_int("COMBS_GEMVD", 1))

@@ -149,6 +149,20 @@ GEMV1_FMT(q8_0, CQ_Q8_0)
 GEMV1_I8_FMT(q4_k, CQ_Q4_K)
 GEMV1_I8_FMT(q4_0, CQ_Q4_0)
 GEMV1_I8_FMT(q8_0, CQ_Q8_0)
+// Rows of 65 to 128 units: each row's halves on a wave pair (gemv1k_body).
+#define GEMV1K_KERNEL(NAME, FMT, YT, EPI)                                                   \
+  extern "C" __global__ void __launch_bounds__(64 * GV1K_WAVES) NAME(const Gv1Args a) { \
+    gemv1k_body<FMT, YT, EPI>(a);                                                       \
+  }
+#define GEMV1K_FMT(fname, FMT)                               \
+  GEMV1K_KERNEL(cq_gemv1k_##fname##_yf32, FMT, 0, 0)         \
+  GEMV1K_KERNEL(cq_gemv1k_##fname##_yf16, FMT, 1, 0)         \
+  GEMV1K_KERNEL(cq_gemv1k_##fname##_yf32_epi, FMT, 0, 1)     \
+  GEMV1K_KERNEL(cq_gemv1k_##fname##_yf16_epi, FMT, 1, 1)
+GEMV1K_FMT(q4_k, CQ_Q4_K)
+GEMV1K_FMT(q5_k, CQ_Q5_K)
+GEMV1K_FMT(q6_k, CQ_Q6_K)
+GEMV1K_FMT(q4_0, CQ_Q4_0)
 
 #ifndef CQ_GV2_DEPTH
 #define CQ_GV2_DEPTH 3

@@ -159,13 +159,14 @@ def test_gate_up_rejects_mismatched_shapes(cuda):
 
 @pytest.mark.parametrize("fmt", KQ)
 @pytest.mark.parametrize("g2", ["0", "2"])
-@pytest.mark.parametrize("n,k", [(140000, 256), (3000, 512), (700, 4096), (300, 5120)])
+@pytest.mark.parametrize("n,k", [(140000, 256), (3000, 512), (700, 4096), (300, 5120), (301, 18944)])
 def test_epilogue_single_row_kernels(cuda, monkeypatch, fmt, g2, n, k):
     """m = 1 epilogues of both single-row kernels: the streaming kernel
     (COMBS_GEMV2=2) preloads each wave's first 64 rows' bias / gate values and
     loads the rest at store time (n = 140000 puts ~68 rows on a wave), with R
     rows per step (k = 256, 512) or several steps per row (k = 5120); the
-    whole-superblock kernel (=0) loads them at store time."""
+    whole-superblock kernel (=0) loads them at store time; k = 18944 runs
+    the half-row wave-pair kernel (cq_gemv1k) either way."""
     import torch
     monkeypatch.setenv("COMBS_GEMV2", g2)
     data, w = _weight(fmt, n, k, 80 + int(fmt))

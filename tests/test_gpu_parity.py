@@ -390,19 +390,29 @@ def test_gemv_batched_gaussian_llama_shape(cuda, fmt, m):
     O.assert_close(got, old, 1e-3, "mfma gemv")
 
 
-@pytest.mark.parametrize("fmt", [QuantFormat.Q4K, QuantFormat.Q6K, QuantFormat.Q4_0, QuantFormat.Q8_0])
-@pytest.mark.parametrize("n,k", [(300, 18944), (67, 16640), (40, 33024)])
-def test_gemv_single_row_long_k(cuda, fmt, n, k):
+@pytest.mark.parametrize("fmt", [QuantFormat.Q4K, QuantFormat.Q5K, QuantFormat.Q6K, QuantFormat.Q4_0, QuantFormat.Q8_0])
+@pytest.mark.parametrize("n,k", [(300, 18944), (67, 16640), (40, 33024), (3, 18944), (37, 27136), (513, 32768),
+                                 (1029, 17152)])
+@pytest.mark.parametrize("kernel", ["gemv1k", "mfma"])
+def test_gemv_single_row_long_k(cuda, monkeypatch, fmt, n, k, kernel):
     """m = 1 with K above the single-row kernels' 16384 (a Qwen2.5-7B down
-    projection is 18944 wide): served by the 16-row MFMA GEMV; fp32 and fp16
-    y, checked against the oracle and for bit-identical repeats."""
+    projection is 18944 wide): rows of 65 to 128 units (106 for Q6_K) on the
+    half-row wave-pair kernel (Q4_K / Q5_K / Q6_K / Q4_0: odd unit counts,
+    Q6_K half rows at every even byte offset, row counts that leave a pair
+    idle), the rest and COMBS_GEMV1K=0 on the 16-row MFMA GEMV; fp32 and
+    fp16 y, checked against the oracle and for bit-identical repeats."""
     import torch
+    monkeypatch.setenv("COMBS_GEMV1K", "1" if kernel == "gemv1k" else "0")
     data = synth(fmt, n, k)
     wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
     w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
     x = O.x_pattern(1, k, 13, 31, 15.0, 16.0).reshape(1, k)
     print(f"long-k {fmt.name} n={n} k={k}", flush=True)
+    # float64 of the oracle's (bit-exact) dequant: at K = 32768 the synthetic
+    # rows cancel to ~1e-5 of their absolute sum, where a sequential fp32 sum
+    # is itself ~1e-3 off
+    expect = x.astype(np.float64) @ wd.astype(np.float64).T
     a = _run(w, x, torch.float16, torch.float32)
-    O.assert_close(a, O.ref_matmul(x, wd), rel_of(fmt), "y32")
+    O.assert_close(a, expect, rel_of(fmt), "y32")
     assert np.array_equal(a.view(np.uint32), _run(w, x, torch.float16, torch.float32).view(np.uint32))
-    O.assert_close(_run(w, x, torch.float16, torch.float16), O.ref_matmul(x, wd), 1e-3, "y16")
+    O.assert_close(_run(w, x, torch.float16, torch.float16), expect, 1e-3, "y16")

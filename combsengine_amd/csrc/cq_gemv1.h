@@ -653,8 +653,8 @@ constexpr int gv1_waves() {
 // epilogue's loads happen at each store (they wait for the weight loads in
 // flight; a slower path kept for outputs with a bias or a gate); EPI = 2:
 // the gated MLP input in one launch, y = act(x . W^T) * (x . W2^T) — a task
-// holds R / 2 rows of the gate W and the same R / 2 rows of the up W2 (units
-// a power of two, R >= 2), so both share one activation staging and the
+// holds floor(R / 2) rows of the gate W and the same rows of the up W2
+// (R >= 2: units <= 32), so both share one activation staging and the
 // product is formed across lanes.
 // The gated Q6_K kernel keeps the int8 path and 4 waves.
 template <int FMT, int EPI>
@@ -720,12 +720,23 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
         if constexpr (EPI == 1) cq_store<YT>(a.y, a.epi, part, r0 + myrow, r0 + myrow);
         else cq_store_raw<YT>(a.y, part, r0 + myrow);
       }
+    } else if constexpr (EPI == 2) {
+      // gate row q and its up row q + half, each summed over the wave
+      for (int q = 0; q < half; q++) {
+        float v = myrow == q ? part : 0.0f, u = myrow == q + half ? part : 0.0f;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+          v += __shfl_xor(v, o, 64);
+          u += __shfl_xor(u, o, 64);
+        }
+        if (lane == 0 && q < nrows) cq_store_raw<YT>(a.y, cq_act(v, a.epi.act) * u, r0 + q);
+      }
     } else {
       for (int q = 0; q < a.rows; q++) {
         float v = myrow == q ? part : 0.0f;
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-        if (lane == 0 && q < nrows) {  // (EPI = 2 is launched for power-of-two units only)
+        if (lane == 0 && q < nrows) {
           if constexpr (EPI == 1) cq_store<YT>(a.y, a.epi, v, r0 + q, r0 + q);
           else cq_store_raw<YT>(a.y, v, r0 + q);
         }

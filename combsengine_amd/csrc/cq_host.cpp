@@ -561,13 +561,13 @@ static cq_status launch_gemv1k(DeviceModule* dm, const cq_weight* w, const void*
   HIP_TRY(hipModuleLaunchKernel(dm->gemv1k[fi][yt][ep], (unsigned)grid, 1, 1, 64 * 4, 1, 1, 0, s, params, nullptr));
   return CQ_OK;
 }
-// The one-launch gated gate/up: a task needs >= 2 rows of power-of-two units.
-static bool gemv1_gated_fits(const cq_weight* w) {
-  const int64_t u = w->k / 256;
-  return gemv1_fits(w) && u <= 32 && (u & (u - 1)) == 0;
+// The one-launch gated gate/up: a task needs >= 2 rows (K / 256 <= 32),
+// and both weights must suit the span loads.
+static bool gemv1_gated_fits(const cq_weight* gate, const cq_weight* up) {
+  return gemv1_fits(gate) && gemv1_fits(up) && gate->k / 256 <= 32;
 }
 // gated (up != null): y = act(x . W^T) * (x . up^T) in one launch; needs
-// K / 256 a power of two up to 32 (gemv1_gated_fits).
+// K / 256 up to 32 (gemv1_gated_fits).
 static cq_status launch_gemv1(DeviceModule* dm, const cq_weight* w, const void* x, void* y, int yt, hipStream_t s,
                               const CqEpi& epi, const cq_weight* up = nullptr) {
   const int fi = fmt_index(w->format);
@@ -835,7 +835,7 @@ cq_status cq_matmul_gate_up(const cq_weight* gate, const cq_weight* up, const vo
   // against one activation staging.  COMBS_GATEUP_FUSED=0 disables it.
   if (!x || !y) return fail(CQ_ERR_NULL, "NULL x or y");
   if (y_dtype != CQ_F16 && y_dtype != CQ_F32) return fail(CQ_ERR_BAD_DTYPE, "y_dtype %d", y_dtype);
-  if (m == 1 && x_dtype == CQ_F16 && gate->format == up->format && gemv1_gated_fits(gate) &&
+  if (m == 1 && x_dtype == CQ_F16 && gate->format == up->format && gemv1_gated_fits(gate, up) &&
       env_int("COMBS_GATEUP_FUSED", 1)) {
     DeviceModule* dm;
     cq_status st = device_module(&dm);

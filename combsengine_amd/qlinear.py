@@ -146,8 +146,10 @@ class QuantWeight:
 
     def __del__(self):
         h = getattr(self, "_h", None)
-        if h is not None and h.value and L._lib is not None:
-            L._lib.cq_weight_destroy(h)
+        # (at interpreter exit the module globals may already be cleared)
+        lib = getattr(L, "_lib", None) if L is not None else None
+        if h is not None and h.value and lib is not None:
+            lib.cq_weight_destroy(h)
             self._h = None
 
     # -- accessors -------------------------------------------------------------

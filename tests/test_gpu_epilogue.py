@@ -188,16 +188,19 @@ ALL_FMTS = FMTS + [QuantFormat.Q4_1, QuantFormat.Q5_1]
 
 
 @pytest.mark.parametrize("fmt", ALL_FMTS)
-@pytest.mark.parametrize("n,k", [(300, 4096), (257, 256), (130, 8192), (45, 1024), (97, 3584)])
+@pytest.mark.parametrize("n,k", [(300, 4096), (257, 256), (130, 8192), (45, 1024), (97, 3584), (50, 768),
+                                 (33, 5120), (40, 16384)])
 @pytest.mark.parametrize("fused", ["1", "0"])
 @pytest.mark.parametrize("y_dt", ["f32", "f16"])
 @pytest.mark.parametrize("spread", ["1", "0"])
 def test_gate_up_single_row_one_launch(cuda, monkeypatch, fmt, n, k, fused, y_dt, spread):
     """m = 1, fp16 x, gate and up of one format: the one-launch kernel (both
-    weights against one activation staging, R/2 gate and R/2 up rows per
-    task, ragged last task) for K/256 a power of two up to 32; K = 3584
-    (14 units) and COMBS_GATEUP_FUSED=0 take the two-launch path.  The fused
-    kernel multiplies the fp32 up product (no fp16 rounding in between)."""
+    weights against one activation staging, floor(R/2) gate and up rows per
+    task, ragged last task; K = 768: 21-row tasks with a lane row left over,
+    K = 3584 / 5120: row sums over the whole wave) for K/256 up to 32 where
+    the weights suit the span loads; K = 16384 (64 units, one row per task)
+    and COMBS_GATEUP_FUSED=0 take the two-launch path.  The fused kernel
+    multiplies the fp32 up product (no fp16 rounding in between)."""
     import torch
     monkeypatch.setenv("COMBS_GATEUP_FUSED", fused)
     monkeypatch.setenv("COMBS_GEMV1_SPREAD", spread)  # tasks wave-major over the grid, or packed
@@ -206,7 +209,12 @@ def test_gate_up_single_row_one_launch(cuda, monkeypatch, fmt, n, k, fused, y_dt
     x = _x(1, k, 96)
     g = O.fused_matmul(int(fmt), gd, x, n, k).astype(np.float64)
     u = O.fused_matmul(int(fmt), ud, x, n, k).astype(np.float64)
-    one_launch = fused == "1" and (k // 256) & (k // 256 - 1) == 0 and k // 256 <= 32
+    units = k // 256
+    unit_bytes = {QuantFormat.Q4K: 144, QuantFormat.Q5K: 176, QuantFormat.Q6K: 210, QuantFormat.Q4_0: 144,
+                  QuantFormat.Q8_0: 272}.get(fmt)
+    spans_ok = unit_bytes is None or (n * units * unit_bytes % 16 == 0 and
+                                      (fmt != QuantFormat.Q6K or units * (64 // units) % 8 == 0))
+    one_launch = fused == "1" and units <= 32 and spans_ok
     if y_dt == "f16" and not one_launch:
         u = u.astype(np.float16).astype(np.float64)
     expect = O.activation(O.ACT_GELU_TANH, g) * u

@@ -477,13 +477,16 @@ static cq_status launch_gemvd(DeviceModule* dm, const cq_weight* w, const void* 
   // NT = 1 below 8192 rows (Qwen2.5 down 3584 x 18944 Q6_K at m = 8: 30.0
   // against 52.7 us with NT = 2), 4 for Q6_K from 32768 rows (lm_head
   // m = 16: 171 against 204 us), else 2; nw = 4, or 2 for NT = 2 above
-  // m = 8, or 8 for NT = 1 up to m = 4 on rows of 32 or more superblocks
-  // (Q4_K 4096 x 14336 at m = 4: 18.6 against 24.0 us).
+  // m = 8, or 8 for NT = 1 up to m = 4 (Q4_K 4096 x 14336 at m = 4: 18.6
+  // against 24.0 us; 512 x 3584 at m = 2: 5.4 against 7.0 us) and up to
+  // m = 8 on rows of fewer than 32 superblocks (512 x 3584 Q4_K / Q6_K:
+  // 6.3 / 8.7 against 7.3 / 8.9 us).
   int nt = w->n < 8192 ? 1 : (w->format == CQ_Q6_K && w->n >= 32768) ? 4 : 2;
   nt = env_int("COMBS_GVD_NT", nt);
   if (nt != 1 && nt != 2 && nt != 4) nt = 2;
   const long long wgs = (w->n + 16 * nt - 1) / (16 * nt);
-  int nw = env_int("COMBS_GVD_WAVES", nt == 2 && m > 8 ? 2 : nt == 1 && m <= 4 && a.units >= 32 ? 8 : 4);
+  const bool eight = nt == 1 && (m <= 4 || (m <= 8 && a.units < 32));
+  int nw = env_int("COMBS_GVD_WAVES", nt == 2 && m > 8 ? 2 : eight ? 8 : 4);
   if (nw < 1 || nw > 8) nw = 4;
   if (nw > a.units) nw = a.units;
   if (wgs > 0x7fffffffLL) return fail(CQ_ERR_BAD_SHAPE, "grid too large (n=%lld)", (long long)w->n);

@@ -304,38 +304,46 @@ def test_graph_capture_replays(cuda, monkeypatch):
     """cq_matmul launches captured into a HIP graph replay correctly, with
     eager work and synchronisations between replays (no memset nodes: the
     library records none).  Captured prefill launches take no K split, so
-    the eager reference is pinned to the unsplit path for bit equality."""
+    the eager reference is pinned to the unsplit path for bit equality.
+    The graph holds single-row decode of a small weight (tasks spread over
+    the grid), batched decode (m = 8), prefill (m = 64) and single-row
+    decode of a 74-superblock Q6_K row (the row-half kernel)."""
     import torch
     monkeypatch.setenv("COMBS_GEMM2_SPLIT", "1")
     fmt, n, k = QuantFormat.Q4K, 512, 4096
     rng = np.random.default_rng(3)
     data = quantize(fmt, rng.normal(0, 0.02, (n, k)).astype(np.float32))
     w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
-    x = torch.from_numpy(rng.normal(0, 1, (1, k)).astype(np.float16)).cuda()
-    xp = torch.from_numpy(rng.normal(0, 1, (64, k)).astype(np.float16)).cuda()
-    y = torch.empty((1, n), dtype=torch.float32, device="cuda")
-    yp = torch.empty((64, n), dtype=torch.float16, device="cuda")
-    w.matmul_into(x, y)
-    w.matmul_into(xp, yp)
+    n2, k2 = 200, 18944
+    w2 = QuantWeight.from_gguf_bytes(QuantFormat.Q6K, quantize(QuantFormat.Q6K, rng.normal(
+        0, 0.02, (n2, k2)).astype(np.float32)), n2, k2)
+    cases = []  # (weight, x, y)
+    for wt, kk, nn, m, dt in ((w, k, n, 1, torch.float32), (w, k, n, 8, torch.float32), (w, k, n, 64, torch.float16),
+                              (w2, k2, n2, 1, torch.float32)):
+        cases.append((wt, torch.from_numpy(rng.normal(0, 1, (m, kk)).astype(np.float16)).cuda(),
+                      torch.empty((m, nn), dtype=dt, device="cuda")))
+    for wt, x, y in cases:
+        wt.matmul_into(x, y)
     torch.cuda.synchronize()
-    ref, refp = y.clone(), yp.clone()
+    refs = [y.clone() for _, _, y in cases]
     g = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         with torch.cuda.graph(g, stream=s):
-            w.matmul_into(x, y)
-            w.matmul_into(xp, yp)
+            for wt, x, y in cases:
+                wt.matmul_into(x, y)
     torch.cuda.current_stream().wait_stream(s)
+    xp = cases[2][1]
     for rep in range(4):
-        y.fill_(float("nan"))
-        yp.fill_(float("nan"))
+        for _, _, y in cases:
+            y.fill_(float("nan"))
         _ = (xp.float() @ xp.float().t()).sum()  # eager work between replays
         torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
-        assert torch.equal(y, ref), rep
-        assert torch.equal(yp, refp), rep
+        for i, (_, _, y) in enumerate(cases):
+            assert torch.equal(y, refs[i]), (rep, i)
 
 
 @pytest.mark.parametrize("fmt", KQ)

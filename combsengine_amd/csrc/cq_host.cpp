@@ -480,12 +480,14 @@ static cq_status launch_gemvd(DeviceModule* dm, const cq_weight* w, const void* 
   // m = 8, or 8 for NT = 1 up to m = 4 (Q4_K 4096 x 14336 at m = 4: 18.6
   // against 24.0 us; 512 x 3584 at m = 2: 5.4 against 7.0 us) and up to
   // m = 8 on rows of fewer than 32 superblocks (512 x 3584 Q4_K / Q6_K:
-  // 6.3 / 8.7 against 7.3 / 8.9 us).
+  // 6.3 / 8.7 against 7.3 / 8.9 us) or in Q4_K on any row (4096 x 14336
+  // at m = 8: 21.0 against 24.2 us; Q5_K / Q6_K there: 27.5 / 30.8 against
+  // 27.0 / 30.2 us, so they keep 4).
   int nt = w->n < 8192 ? 1 : (w->format == CQ_Q6_K && w->n >= 32768) ? 4 : 2;
   nt = env_int("COMBS_GVD_NT", nt);
   if (nt != 1 && nt != 2 && nt != 4) nt = 2;
   const long long wgs = (w->n + 16 * nt - 1) / (16 * nt);
-  const bool eight = nt == 1 && (m <= 4 || (m <= 8 && a.units < 32));
+  const bool eight = nt == 1 && (m <= 4 || (m <= 8 && (a.units < 32 || w->format == CQ_Q4_K)));
   int nw = env_int("COMBS_GVD_WAVES", nt == 2 && m > 8 ? 2 : eight ? 8 : 4);
   if (nw < 1 || nw > 8) nw = 4;
   if (nw > a.units) nw = a.units;

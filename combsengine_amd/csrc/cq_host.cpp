@@ -483,7 +483,12 @@ static cq_status launch_gemvd(DeviceModule* dm, const cq_weight* w, const void* 
   // 6.3 / 8.7 against 7.3 / 8.9 us) or in Q4_K on any row (4096 x 14336
   // at m = 8: 21.0 against 24.2 us; Q5_K / Q6_K there: 27.5 / 30.8 against
   // 27.0 / 30.2 us, so they keep 4).
-  int nt = w->n < 8192 ? 1 : (w->format == CQ_Q6_K && w->n >= 32768) ? 4 : 2;
+  // Below 8192 rows, Q4_K / Q5_K rows of 32+ superblocks above m = 8 also
+  // take two tiles (4096 x 14336 at m = 16: Q5_K 32.3 against 34.6 us,
+  // Q4_K 26.3 against 26.7; Q6_K 3584 x 18944 and 3584 x 3584 Q4_K are
+  // slower with two).
+  const bool two_short = m > 8 && a.units >= 32 && (w->format == CQ_Q4_K || w->format == CQ_Q5_K);
+  int nt = w->n < 8192 ? (two_short ? 2 : 1) : (w->format == CQ_Q6_K && w->n >= 32768) ? 4 : 2;
   nt = env_int("COMBS_GVD_NT", nt);
   if (nt != 1 && nt != 2 && nt != 4) nt = 2;
   const long long wgs = (w->n + 16 * nt - 1) / (16 * nt);

@@ -699,7 +699,11 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
   const long long slots = (long long)dm->cus * (mt == 8 && nw == 4 ? 2 : 1);
   const long long mblk = (m + 16 * mt - 1) / (16 * mt);
   int nt = env_int("COMBS_GEMM2_NT", 0);
-  if (nt != 1 && nt != 2) nt = (w->n + 16 * nw - 1) / (16 * nw) * mblk * 2 >= slots ? 2 : 1;  // NT = 2 while it fills half the slots
+  // NT = 2 while it fills half the slots; Q6_K (long K per superblock pass)
+  // already from three eighths (3584 x 18944 at m = 512: 165 against 173 us;
+  // Q4_K 14336 x 4096 at m = 128 stays faster with one tile, 46.6 against 50.9).
+  const long long fill = (w->n + 16 * nw - 1) / (16 * nw) * mblk * 2;
+  if (nt != 1 && nt != 2) nt = (w->format == CQ_Q6_K ? fill * 4 >= slots * 3 : fill >= slots) ? 2 : 1;
   const long long gx = (w->n + 16 * nw * nt - 1) / (16 * nw * nt);
   if (gx > 0x7fffffffLL || mblk > 65535) return fail(CQ_ERR_BAD_SHAPE, "grid too large");
   // Split K when the tiles leave compute units idle (each slice keeps >= 3

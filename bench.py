@@ -201,9 +201,11 @@ def secondary(dev):
     res = {}
     for mode in ("1", "0"):
         os.environ["COMBS_GATEUP_FUSED"] = mode
+        L.reload_options()
         us, _ = graph_time_us(gate_up, 2 * len(gpool))
         res["one_launch" if mode == "1" else "two_launches"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1)}
     os.environ.pop("COMBS_GATEUP_FUSED")
+    L.reload_options()
     out["gate_up_silu_q4_k_14336x4096_m1"] = res
     del gpool, upool
     # decode batch 4 / 16 on the gate shape

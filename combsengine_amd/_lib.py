@@ -15,7 +15,7 @@ EXPORTS = (
     "cq_block_values", "cq_block_bytes", "cq_tensor_bytes", "cq_weight_create",
     "cq_weight_wrap_device", "cq_weight_destroy", "cq_weight_dims", "cq_weight_vram_bytes",
     "cq_weight_device_ptr", "cq_matmul", "cq_matmul_path", "cq_matmul_bias", "cq_matmul_gate_up",
-    "cq_dequantize", "cq_quantize",
+    "cq_dequantize", "cq_quantize", "cq_matmul_kernels", "cq_reload_options",
     "cq_last_error", "cq_version",
 )
 
@@ -57,6 +57,8 @@ def lib():
         "cq_matmul_gate_up": ([P, P, P, i32, i64, i32, P, i32, P], i32),
         "cq_dequantize": ([i32, P, sz, i64, P, P], i32),
         "cq_quantize": ([i32, P, i64, i64, P, sz, i32], i32),
+        "cq_matmul_kernels": ([P, i32, i64, i32, ctypes.c_char_p, sz], i32),
+        "cq_reload_options": ([], None),
         "cq_last_error": ([], ctypes.c_char_p),
         "cq_version": ([], ctypes.c_char_p),
     }
@@ -70,3 +72,24 @@ def lib():
 
 def last_error() -> str:
     return lib().cq_last_error().decode(errors="replace")
+
+
+def reload_options() -> None:
+    """Re-read the COMBS_* tuning variables (the library reads them once)."""
+    lib().cq_reload_options()
+
+
+def kernels(weight, x_dtype: int, m: int, y_dtype: int) -> str:
+    """Names of the kernels cq_matmul launches for this call shape."""
+    buf = ctypes.create_string_buffer(512)
+    st = lib().cq_matmul_kernels(weight.handle, x_dtype, m, y_dtype, buf, 512)
+    if st != CQ_OK:
+        raise RuntimeError(last_error())
+    return buf.value.decode()
+
+
+def path_name(weight, x, y) -> str:
+    """kernels() for device tensors x [m, k] and y [m, n]."""
+    xt = CQ_F16 if str(x.dtype) == "torch.float16" else CQ_F32
+    yt = CQ_F16 if str(y.dtype) == "torch.float16" else CQ_F32
+    return kernels(weight, xt, x.shape[0], yt)

@@ -1,10 +1,11 @@
 """Build recipe for the gfx950 library (no cmake/ninja needed).
 
-1. hipcc --genco compiles csrc/cq_kernels.hip (all device code) into one
-   gfx950 code object, lib/cq_gfx950.hsaco.
+1. hipcc --genco compiles each csrc/cq_k_*.hip (the device code, split in
+   four translation units that compile in parallel) into a gfx950 code
+   object, lib/cq_k_*.hsaco.
 2. g++ compiles the host side (C ABI, module loading, quantisers) into
-   lib/libcombs_qlinear.so, embedding the code object with .incbin, and links
-   the HIP runtime (libamdhip64).
+   lib/libcombs_qlinear.so, embedding the code objects with .incbin, and
+   links the HIP runtime (libamdhip64).
 
 The .so is self-contained: it loads its kernels with hipModuleLoadData at
 first use on each device.
@@ -16,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIBDIR = os.path.join(HERE, "lib")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
-HSACO = os.path.join(LIBDIR, "cq_gfx950.hsaco")
+OBJECTS = ("gemv", "gemv1", "gemv2", "gemm")  # csrc/cq_k_<name>.hip -> lib/cq_k_<name>.hsaco
 SO = os.path.join(LIBDIR, "libcombs_qlinear.so")
 
 HIPCC_FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17",
@@ -40,10 +41,28 @@ def _run(cmd, verbose):
 
 def build(verbose: bool = False) -> str:
     os.makedirs(LIBDIR, exist_ok=True)
-    _run([os.path.join(ROCM, "bin", "hipcc"), "--genco", *HIPCC_FLAGS,
-          os.path.join(CSRC, "cq_kernels.hip"), "-o", HSACO], verbose)
+    procs = []
+    for name in OBJECTS:
+        cmd = [os.path.join(ROCM, "bin", "hipcc"), "--genco", *HIPCC_FLAGS,
+               os.path.join(CSRC, f"cq_k_{name}.hip"), "-o", os.path.join(LIBDIR, f"cq_k_{name}.hsaco")]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
+    failed = []
+    for cmd, p in procs:
+        _, err = p.communicate()
+        err = "\n".join(l for l in err.splitlines() if "packed-fp32-ops" not in l)
+        if p.returncode != 0:
+            failed.append(f"build failed: {' '.join(cmd)}\n{err}")
+        elif verbose and err.strip():
+            print(err[-4000:])
+    if failed:
+        raise RuntimeError("\n".join(failed))
+    stale = os.path.join(LIBDIR, "cq_gfx950.hsaco")  # the former single code object
+    if os.path.exists(stale):
+        os.remove(stale)
     _run(["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-fopenmp", "-Wall",
-          "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", f'-DCQ_HSACO_PATH="{HSACO}"',
+          "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", f'-DCQ_HSACO_DIR="{LIBDIR}"',
           os.path.join(CSRC, "cq_host.cpp"), os.path.join(CSRC, "cq_quantize.cpp"),
           f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-o", SO], verbose)
     return SO

@@ -164,8 +164,19 @@ __device__ __forceinline__ float cq_act(float v, int act) {
   }
   return 0.5f * v * (1.0f + erff(v * 0.7071067811865476f));
 }
+// A projection's output in y's dtype: the reference's fp16 model casts each
+// op's fp32 result to fp16 before the bias add or the gated product
+// (qlinear.rs:84-98, 126-143; llama.rs:301-303), so with fp16 y the
+// epilogues round the accumulator first.
+template <int YT>
+__device__ __forceinline__ float cq_round_y(float v) {
+  return YT ? (float)(_Float16)v : v;
+}
 // idx: flat index of the output element [m][n]; n: its column.
+template <int YT>
 __device__ __forceinline__ float cq_epilogue(const CqEpi& e, float v, size_t idx, int n) {
+  if (!e.bias && !e.aux) return v;
+  v = cq_round_y<YT>(v);
   if (e.bias) v += e.bias_f16 ? (float)((const _Float16*)e.bias)[n] : ((const float*)e.bias)[n];
   if (e.aux) {
     const float u = e.aux_f16 ? (float)((const _Float16*)e.aux)[idx] : ((const float*)e.aux)[idx];
@@ -177,10 +188,19 @@ __device__ __forceinline__ float cq_epilogue(const CqEpi& e, float v, size_t idx
 // parts are ignored).  Streaming kernels load them ahead of their weight
 // stream: a load at store time would make the in-order load counter wait for
 // every weight load still in flight.
+template <int YT>
 __device__ __forceinline__ float cq_epi_apply(const CqEpi& e, float v, float b, float u) {
+  if (!e.bias && !e.aux) return v;
+  v = cq_round_y<YT>(v);
   if (e.bias) v += b;
   if (e.aux) v = cq_act(v, e.act) * u;
   return v;
+}
+// The one-launch gated product act(g) * u of two fp32 projections, each
+// first rounded to y's dtype.
+template <int YT>
+__device__ __forceinline__ float cq_gated(float g, float u, int act) {
+  return cq_act(cq_round_y<YT>(g), act) * cq_round_y<YT>(u);
 }
 __device__ __forceinline__ float cq_epi_bias(const CqEpi& e, int n) {
   if (!e.bias) return 0.0f;
@@ -198,7 +218,7 @@ __device__ __forceinline__ void cq_store_raw(void* y, float v, size_t idx) {
 // Stores one output element through the epilogue.
 template <int YT>
 __device__ __forceinline__ void cq_store(void* y, const CqEpi& e, float v, size_t idx, int n) {
-  v = cq_epilogue(e, v, idx, n);
+  v = cq_epilogue<YT>(e, v, idx, n);
   if (YT) ((_Float16*)y)[idx] = (_Float16)v;
   else ((float*)y)[idx] = v;
 }

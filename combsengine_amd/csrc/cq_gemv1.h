@@ -715,7 +715,7 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
         // up row rq sits half * units lanes after its gate row
         const float upv = __shfl(part, (lane + half * a.units) & 63, 64);
         if (myunit == 0 && myrow < half && rq < nrows)
-          cq_store_raw<YT>(a.y, cq_act(part, a.epi.act) * upv, r0 + rq);
+          cq_store_raw<YT>(a.y, cq_gated<YT>(part, upv, a.epi.act), r0 + rq);
       } else if (myunit == 0 && myrow < nrows) {
         if constexpr (EPI == 1) cq_store<YT>(a.y, a.epi, part, r0 + myrow, r0 + myrow);
         else cq_store_raw<YT>(a.y, part, r0 + myrow);
@@ -729,7 +729,7 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
           v += __shfl_xor(v, o, 64);
           u += __shfl_xor(u, o, 64);
         }
-        if (lane == 0 && q < nrows) cq_store_raw<YT>(a.y, cq_act(v, a.epi.act) * u, r0 + q);
+        if (lane == 0 && q < nrows) cq_store_raw<YT>(a.y, cq_gated<YT>(v, u, a.epi.act), r0 + q);
       }
     } else {
       for (int q = 0; q < a.rows; q++) {

@@ -250,7 +250,7 @@ __device__ __forceinline__ void gemv2_body(const Gv2Args& a) {
         b = cq_epi_bias(a.epi, min(row, a.N - 1));
         u = cq_epi_aux(a.epi, min(row, a.N - 1));
       }
-      v = cq_epi_apply(a.epi, v, b, u);
+      v = cq_epi_apply<YT>(a.epi, v, b, u);
     }
     if (leader) cq_store_raw<YT>(a.y, v, row);
   };

@@ -14,25 +14,29 @@
 #include <functional>
 #include <mutex>
 #include <string>
+#include <unordered_map>
 
 #include "../../include/combs_qlinear.h"
 #include "cq_epi.h"
 
-#ifndef CQ_HSACO_PATH
-#error "CQ_HSACO_PATH must name the gfx950 code object to embed"
+#ifndef CQ_HSACO_DIR
+#error "CQ_HSACO_DIR must name the directory of the gfx950 code objects to embed"
 #endif
 
-__asm__(".section .rodata\n"
-        ".global cq_hsaco_image\n"
-        ".balign 4096\n"
-        "cq_hsaco_image:\n"
-        ".incbin \"" CQ_HSACO_PATH "\"\n"
-        ".global cq_hsaco_image_end\n"
-        "cq_hsaco_image_end:\n"
-        ".byte 0\n"
-        ".previous\n");
-extern "C" const unsigned char cq_hsaco_image[];
-extern "C" const unsigned char cq_hsaco_image_end[];
+// The four code objects built from csrc/cq_k_*.hip, embedded read-only.
+#define CQ_EMBED(NAME)                                      \
+  __asm__(".section .rodata\n"                              \
+          ".global cq_hsaco_" #NAME "\n"                     \
+          ".balign 4096\n"                                  \
+          "cq_hsaco_" #NAME ":\n"                            \
+          ".incbin \"" CQ_HSACO_DIR "/cq_k_" #NAME ".hsaco\"\n" \
+          ".byte 0\n"                                       \
+          ".previous\n");                                   \
+  extern "C" const unsigned char cq_hsaco_##NAME[];
+CQ_EMBED(gemv)
+CQ_EMBED(gemv1)
+CQ_EMBED(gemv2)
+CQ_EMBED(gemm)
 
 namespace {
 
@@ -172,7 +176,8 @@ struct DeviceModule {
   std::once_flag once;
   cq_status status = CQ_ERR_NO_DEVICE;
   std::string err;
-  hipModule_t mod = nullptr;
+  hipModule_t mods[4] = {};
+  std::unordered_map<hipFunction_t, std::string> names;  // kernel name of each looked-up function
   hipFunction_t gemv[kNumFormats][2][2] = {};  // [format][x f32][y f16]
   hipFunction_t dequant[kNumFormats] = {};
   hipFunction_t gemm[kNumFormats][2][2] = {};  // K-quant formats only
@@ -199,18 +204,35 @@ void load_module(DeviceModule& d, int dev) {
     return;
   }
   d.cus = prop.multiProcessorCount;
-  hipError_t e = hipModuleLoadData(&d.mod, cq_hsaco_image);
-  if (e != hipSuccess) {
-    d.err = std::string("hipModuleLoadData: ") + hipGetErrorString(e);
-    return;
+  const unsigned char* images[4] = {cq_hsaco_gemv, cq_hsaco_gemv1, cq_hsaco_gemv2, cq_hsaco_gemm};
+  for (int i = 0; i < 4; i++) {
+    hipError_t e = hipModuleLoadData(&d.mods[i], images[i]);
+    if (e != hipSuccess) {
+      d.err = std::string("hipModuleLoadData: ") + hipGetErrorString(e);
+      return;
+    }
   }
+  // a kernel by name from the code object that holds it (cq_k_gemv: the
+  // 16-row and batched GEMVs and the dequant kernels; cq_k_gemv1: cq_gemv1*;
+  // cq_k_gemv2: cq_gemv2*; cq_k_gemm: the prefill kernels).  Only the right
+  // object is asked: a failed lookup would leave an error in the runtime's
+  // last-error state for the caller's next check to find.
+  auto get = [&d](hipFunction_t* f, const char* nm) {
+    const std::string n(nm);
+    const int mi = n.rfind("cq_gemv1", 0) == 0 ? 1 : n.rfind("cq_gemv2", 0) == 0 ? 2
+                   : (n.rfind("cq_gemm", 0) == 0 || n.rfind("cq_xsums", 0) == 0 || n.rfind("cq_splitk", 0) == 0) ? 3
+                   : 0;
+    const hipError_t e = hipModuleGetFunction(f, d.mods[mi], nm);
+    if (e == hipSuccess) d.names[*f] = nm;
+    return e;
+  };
   char name[96];
   for (int fi = 0; fi < kNumFormats; fi++) {
     const char* fn = fmt_name(kFormats[fi]);
     for (int xt = 0; xt < 2; xt++)
       for (int yt = 0; yt < 2; yt++) {
         snprintf(name, sizeof name, "cq_gemv_%s_x%s_y%s", fn, xt ? "f32" : "f16", yt ? "f16" : "f32");
-        if (hipModuleGetFunction(&d.gemv[fi][xt][yt], d.mod, name) != hipSuccess) {
+        if (get(&d.gemv[fi][xt][yt], name) != hipSuccess) {
           d.err = std::string("missing kernel ") + name;
           return;
         }
@@ -219,7 +241,7 @@ void load_module(DeviceModule& d, int dev) {
       for (int xt = 0; xt < 2; xt++)
         for (int yt = 0; yt < 2; yt++) {
           snprintf(name, sizeof name, "cq_gemm_%s_x%s_y%s", fn, xt ? "f32" : "f16", yt ? "f16" : "f32");
-          if (hipModuleGetFunction(&d.gemm[fi][xt][yt], d.mod, name) != hipSuccess) {
+          if (get(&d.gemm[fi][xt][yt], name) != hipSuccess) {
             d.err = std::string("missing kernel ") + name;
             return;
           }
@@ -228,14 +250,14 @@ void load_module(DeviceModule& d, int dev) {
         for (int mt = 8; mt <= 16; mt += 8)
           for (int yt = 0; yt < 2; yt++) {
             snprintf(name, sizeof name, "cq_gemm2_%s_n%d_m%d_y%s", fn, nt, mt, yt ? "f16" : "f32");
-            if (hipModuleGetFunction(&d.gemm2[fi][nt - 1][mt / 8 - 1][yt], d.mod, name) != hipSuccess) {
+            if (get(&d.gemm2[fi][nt - 1][mt / 8 - 1][yt], name) != hipSuccess) {
               d.err = std::string("missing kernel ") + name;
               return;
             }
           }
     }
     snprintf(name, sizeof name, "cq_dequant_%s", fn);
-    if (hipModuleGetFunction(&d.dequant[fi], d.mod, name) != hipSuccess) {
+    if (get(&d.dequant[fi], name) != hipSuccess) {
       d.err = std::string("missing kernel ") + name;
       return;
     }
@@ -245,21 +267,21 @@ void load_module(DeviceModule& d, int dev) {
       for (int ep = 0; ep < 3; ep++) {
         static const char* const kEpi[3] = {"", "_epi", "_gated"};
         snprintf(name, sizeof name, "cq_gemv1_%s_y%s%s", fmt_name(kFormats[fi]), yt ? "f16" : "f32", kEpi[ep]);
-        if (hipModuleGetFunction(&d.gemv1[fi][yt][ep], d.mod, name) != hipSuccess) {
+        if (get(&d.gemv1[fi][yt][ep], name) != hipSuccess) {
           d.err = std::string("missing kernel ") + name;
           return;
         }
         const int f = kFormats[fi];
         if (ep < 2 && (f == CQ_Q4_K || f == CQ_Q4_0 || f == CQ_Q8_0)) {
           snprintf(name, sizeof name, "cq_gemv1_%s_y%s%s_i8", fmt_name(f), yt ? "f16" : "f32", ep ? "_epi" : "");
-          if (hipModuleGetFunction(&d.gemv1_i8[fi][yt][ep], d.mod, name) != hipSuccess) {
+          if (get(&d.gemv1_i8[fi][yt][ep], name) != hipSuccess) {
             d.err = std::string("missing kernel ") + name;
             return;
           }
         }
         if (ep < 2 && (f == CQ_Q4_K || f == CQ_Q5_K || f == CQ_Q6_K || f == CQ_Q4_0)) {
           snprintf(name, sizeof name, "cq_gemv1k_%s_y%s%s", fmt_name(f), yt ? "f16" : "f32", ep ? "_epi" : "");
-          if (hipModuleGetFunction(&d.gemv1k[fi][yt][ep], d.mod, name) != hipSuccess) {
+          if (get(&d.gemv1k[fi][yt][ep], name) != hipSuccess) {
             d.err = std::string("missing kernel ") + name;
             return;
           }
@@ -268,28 +290,29 @@ void load_module(DeviceModule& d, int dev) {
         if (ep == 0)
           for (int nt = 0; nt < 3; nt++) {
             snprintf(name, sizeof name, "cq_gemvd_%s_n%d_y%s", fmt_name(kFormats[fi]), 1 << nt, yt ? "f16" : "f32");
-            if (hipModuleGetFunction(&d.gemvd[fi][nt][yt], d.mod, name) != hipSuccess) {
+            if (get(&d.gemvd[fi][nt][yt], name) != hipSuccess) {
               d.err = std::string("missing kernel ") + name;
               return;
             }
           }
         if (ep == 2) continue;
         snprintf(name, sizeof name, "cq_gemv2_%s_y%s%s", fmt_name(kFormats[fi]), yt ? "f16" : "f32", ep ? "_epi" : "");
-        if (hipModuleGetFunction(&d.gemv2[fi][yt][ep], d.mod, name) != hipSuccess) {
+        if (get(&d.gemv2[fi][yt][ep], name) != hipSuccess) {
           d.err = std::string("missing kernel ") + name;
           return;
         }
       }
   }
-  if (hipModuleGetFunction(&d.reduce[0], d.mod, "cq_splitk_reduce_yf32") != hipSuccess ||
-      hipModuleGetFunction(&d.reduce[1], d.mod, "cq_splitk_reduce_yf16") != hipSuccess) {
+  if (get(&d.reduce[0], "cq_splitk_reduce_yf32") != hipSuccess ||
+      get(&d.reduce[1], "cq_splitk_reduce_yf16") != hipSuccess) {
     d.err = "missing kernel cq_splitk_reduce_*";
     return;
   }
-  if (hipModuleGetFunction(&d.xsums, d.mod, "cq_xsums_f16") != hipSuccess) {
+  if (get(&d.xsums, "cq_xsums_f16") != hipSuccess) {
     d.err = "missing kernel cq_xsums_f16";
     return;
   }
+  (void)hipGetLastError();  // leave no lookup status behind for the caller's checks
   d.status = CQ_OK;
 }
 
@@ -305,9 +328,63 @@ cq_status device_module(DeviceModule** out) {
   return CQ_OK;
 }
 
+// Tuning and A/B knobs (COMBS_* environment variables), read once at the
+// first launch and again only on cq_reload_options(): a launch never calls
+// getenv.  kUnset marks "use the shape rule".
+constexpr int kUnset = -1000000;
+struct Knobs {
+  int gemv_waves, gemv1, gemv1k, gemv1_grid, gemv1_i8, gemv1_prefetch2, gemv1_span, gemv1_spread,
+      gemv1_wave_major, gemv2, gemv2_wpc, gemvd, gvd_nt, gvd_waves, gemm_kernel, gemm_waves, gemm2_mt,
+      gemm2_nt, gemm2_split, gateup_fused;
+};
+Knobs g_knobs;
+std::once_flag g_knobs_once;
+
 int env_int(const char* name, int dflt) {
   const char* v = getenv(name);
   return (v && *v) ? atoi(v) : dflt;
+}
+void read_knobs() {
+  Knobs k;
+  k.gemv_waves = env_int("COMBS_GEMV_WAVES", 0);
+  k.gemv1 = env_int("COMBS_GEMV1", 1);
+  k.gemv1k = env_int("COMBS_GEMV1K", 1);
+  k.gemv1_grid = env_int("COMBS_GEMV1_GRID", kUnset);
+  k.gemv1_i8 = env_int("COMBS_GEMV1_I8", 1);
+  k.gemv1_prefetch2 = env_int("COMBS_GEMV1_PREFETCH2", 0);
+  k.gemv1_span = env_int("COMBS_GEMV1_SPAN", 1);
+  k.gemv1_spread = env_int("COMBS_GEMV1_SPREAD", 1);
+  k.gemv1_wave_major = env_int("COMBS_GEMV1_WAVE_MAJOR", 0);
+  k.gemv2 = env_int("COMBS_GEMV2", 0);
+  k.gemv2_wpc = env_int("COMBS_GEMV2_WPC", 1);
+  k.gemvd = env_int("COMBS_GEMVD", 1);
+  k.gvd_nt = env_int("COMBS_GVD_NT", kUnset);
+  k.gvd_waves = env_int("COMBS_GVD_WAVES", kUnset);
+  k.gemm_kernel = env_int("COMBS_GEMM_KERNEL", 2);
+  k.gemm_waves = env_int("COMBS_GEMM_WAVES", 4);
+  k.gemm2_mt = env_int("COMBS_GEMM2_MT", 0);
+  k.gemm2_nt = env_int("COMBS_GEMM2_NT", 0);
+  k.gemm2_split = env_int("COMBS_GEMM2_SPLIT", 0);
+  k.gateup_fused = env_int("COMBS_GATEUP_FUSED", 1);
+  g_knobs = k;
+}
+const Knobs& knobs() {
+  std::call_once(g_knobs_once, read_knobs);
+  return g_knobs;
+}
+
+// Dry runs (cq_matmul_kernels): while set, launches record the kernel name
+// instead of running and no scratch memory is allocated.
+thread_local std::string* g_plan = nullptr;
+
+hipError_t klaunch(DeviceModule* dm, hipFunction_t f, unsigned gx, unsigned gy, unsigned gz, unsigned block,
+                   unsigned lds, hipStream_t s, void** params) {
+  if (g_plan) {
+    if (!g_plan->empty()) *g_plan += ",";
+    *g_plan += dm->names[f];
+    return hipSuccess;
+  }
+  return hipModuleLaunchKernel(f, gx, gy, gz, block, 1, 1, lds, s, params, nullptr);
 }
 
 }  // namespace
@@ -412,7 +489,7 @@ constexpr int kGemvDepth = 4;
 constexpr int kGemvLdsBudget = 56 * 1024;
 
 static int gemv_waves(int units) {
-  int nw = env_int("COMBS_GEMV_WAVES", 0);
+  int nw = knobs().gemv_waves;
   if (nw >= 1 && nw <= 8) return nw;
   // one group of kGemvDepth units per wave where possible, at most 8 waves
   nw = (units + kGemvDepth - 1) / kGemvDepth;
@@ -450,8 +527,8 @@ static cq_status launch_gemv(DeviceModule* dm, const cq_weight* w, const void* x
     return fail(CQ_ERR_BAD_SHAPE, "grid too large (n=%lld, m=%lld)", (long long)w->n, (long long)m);
   const int nw = gemv_waves(a.units);
   void* params[] = {&a};
-  HIP_TRY(hipModuleLaunchKernel(dm->gemv[fi][xt][yt], (unsigned)row_tiles, (unsigned)m_tiles, 1, 64 * nw, 1, 1,
-                                (unsigned)lds, s, params, nullptr));
+  HIP_TRY(klaunch(dm, dm->gemv[fi][xt][yt], (unsigned)row_tiles, (unsigned)m_tiles, 1, 64 * nw, (unsigned)lds, s,
+                  params));
   return CQ_OK;
 }
 
@@ -489,17 +566,17 @@ static cq_status launch_gemvd(DeviceModule* dm, const cq_weight* w, const void* 
   // slower with two).
   const bool two_short = m > 8 && a.units >= 32 && (w->format == CQ_Q4_K || w->format == CQ_Q5_K);
   int nt = w->n < 8192 ? (two_short ? 2 : 1) : (w->format == CQ_Q6_K && w->n >= 32768) ? 4 : 2;
-  nt = env_int("COMBS_GVD_NT", nt);
+  if (knobs().gvd_nt != kUnset) nt = knobs().gvd_nt;
   if (nt != 1 && nt != 2 && nt != 4) nt = 2;
   const long long wgs = (w->n + 16 * nt - 1) / (16 * nt);
   const bool eight = nt == 1 && (m <= 4 || (m <= 8 && (a.units < 32 || w->format == CQ_Q4_K)));
-  int nw = env_int("COMBS_GVD_WAVES", nt == 2 && m > 8 ? 2 : eight ? 8 : 4);
+  int nw = knobs().gvd_waves != kUnset ? knobs().gvd_waves : nt == 2 && m > 8 ? 2 : eight ? 8 : 4;
   if (nw < 1 || nw > 8) nw = 4;
   if (nw > a.units) nw = a.units;
   if (wgs > 0x7fffffffLL) return fail(CQ_ERR_BAD_SHAPE, "grid too large (n=%lld)", (long long)w->n);
   void* params[] = {&a};
-  HIP_TRY(hipModuleLaunchKernel(dm->gemvd[fi][nt == 1 ? 0 : nt == 2 ? 1 : 2][yt], (unsigned)wgs, 1, 1, 64 * nw, 1,
-                                1, 0, s, params, nullptr));
+  HIP_TRY(klaunch(dm, dm->gemvd[fi][nt == 1 ? 0 : nt == 2 ? 1 : 2][yt], (unsigned)wgs, 1, 1, 64 * nw, 0, s,
+                  params));
   return CQ_OK;
 }
 
@@ -568,7 +645,7 @@ static cq_status launch_gemv1k(DeviceModule* dm, const cq_weight* w, const void*
   const int64_t need = (w->n + kPairs - 1) / kPairs;
   const int grid = (int)(need < dm->cus ? need : dm->cus);
   void* params[] = {&a};
-  HIP_TRY(hipModuleLaunchKernel(dm->gemv1k[fi][yt][ep], (unsigned)grid, 1, 1, 64 * 4, 1, 1, 0, s, params, nullptr));
+  HIP_TRY(klaunch(dm, dm->gemv1k[fi][yt][ep], (unsigned)grid, 1, 1, 64 * 4, 0, s, params));
   return CQ_OK;
 }
 // The one-launch gated gate/up: a task needs >= 2 rows (K / 256 <= 32),
@@ -593,9 +670,9 @@ static cq_status launch_gemv1(DeviceModule* dm, const cq_weight* w, const void* 
   a.rows = a.units >= 64 ? 1 : 64 / a.units;
   const int per_task = up ? a.rows / 2 : a.rows;
   a.tasks = (int)((w->n + per_task - 1) / per_task);
-  a.prefetch2 = env_int("COMBS_GEMV1_PREFETCH2", 0);
-  a.span = env_int("COMBS_GEMV1_SPAN", 1);
-  a.wave_major = env_int("COMBS_GEMV1_WAVE_MAJOR", 0);
+  a.prefetch2 = knobs().gemv1_prefetch2;
+  a.span = knobs().gemv1_span;
+  a.wave_major = knobs().gemv1_wave_major;
   a.epi = epi;
   const int ep = up ? 2 : (epi.bias || epi.aux) ? 1 : 0;
   // Weights with fewer workgroups of tasks than compute units spread their
@@ -609,9 +686,9 @@ static cq_status launch_gemv1(DeviceModule* dm, const cq_weight* w, const void* 
   // 0 never, 2 whenever the weight is small.
   hipFunction_t k = dm->gemv1[fi][yt][ep];
   int nw = gemv1_waves(w->format, up != nullptr);
-  int cap = env_int("COMBS_GEMV1_GRID", dm->cus);
+  int cap = knobs().gemv1_grid != kUnset ? knobs().gemv1_grid : dm->cus;
   if (cap < 1) cap = 1;
-  const int i8 = env_int("COMBS_GEMV1_I8", 1);
+  const int i8 = knobs().gemv1_i8;
   const int i8w = w->format == CQ_Q4_K ? 8 : 4;  // the _i8 kernels' waves
   if (ep < 2 && dm->gemv1_i8[fi][yt][ep] && a.tasks <= (int64_t)cap * i8w &&
       (i8 == 2 || (i8 == 1 && w->format != CQ_Q4_K && a.tasks > cap))) {
@@ -625,12 +702,12 @@ static cq_status launch_gemv1(DeviceModule* dm, const cq_weight* w, const void* 
   // 9.4-9.7; Q5_K 11.6 against 11.8-12.1).
   const int rounds = (wgs + cap - 1) / cap;
   int grid = (wgs + rounds - 1) / rounds;
-  if (env_int("COMBS_GEMV1_SPREAD", 1) && wgs < cap) {
+  if (knobs().gemv1_spread && wgs < cap) {
     a.wave_major = 1;
     grid = a.tasks < cap ? a.tasks : cap;
   }
   void* params[] = {&a};
-  HIP_TRY(hipModuleLaunchKernel(k, (unsigned)grid, 1, 1, 64 * nw, 1, 1, 0, s, params, nullptr));
+  HIP_TRY(klaunch(dm, k, (unsigned)grid, 1, 1, 64 * nw, 0, s, params));
   return CQ_OK;
 }
 
@@ -654,7 +731,7 @@ static cq_status launch_gemv2(DeviceModule* dm, const cq_weight* w, const void* 
   a.C = a.R > 1 ? 1 : (a.units + 15) / 16;
   a.cinv = (65536 + a.C - 1) / a.C;
   a.epi = epi;
-  int wpc = env_int("COMBS_GEMV2_WPC", 1);
+  int wpc = knobs().gemv2_wpc;
   if (wpc < 1 || wpc > 2) wpc = 1;
   // waves: a few steps each where the weight allows, never more than rows
   const long long row_groups = (a.N + a.R - 1) / a.R;
@@ -666,7 +743,7 @@ static cq_status launch_gemv2(DeviceModule* dm, const cq_weight* w, const void* 
   if ((long long)a.N * a.C / a.waves + a.C > 16384) return fail(CQ_ERR_BAD_SHAPE, "gemv2: too many rows per wave");
   void* params[] = {&a};
   const int ep = epi.bias || epi.aux;
-  HIP_TRY(hipModuleLaunchKernel(dm->gemv2[fi][yt][ep], (unsigned)grid, 1, 1, 64 * kGv2Waves, 1, 1, 0, s, params, nullptr));
+  HIP_TRY(klaunch(dm, dm->gemv2[fi][yt][ep], (unsigned)grid, 1, 1, 64 * kGv2Waves, 0, s, params));
   return CQ_OK;
 }
 
@@ -693,12 +770,12 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
   a.part = nullptr;
   a.usplit = a.units;
   a.epi = epi;
-  int mt = env_int("COMBS_GEMM2_MT", 0);
+  int mt = knobs().gemm2_mt;
   if (mt != 8 && mt != 16) mt = 8;
   const int nw = 4;  // waves per workgroup (the kernels' launch bounds)
   const long long slots = (long long)dm->cus * (mt == 8 && nw == 4 ? 2 : 1);
   const long long mblk = (m + 16 * mt - 1) / (16 * mt);
-  int nt = env_int("COMBS_GEMM2_NT", 0);
+  int nt = knobs().gemm2_nt;
   // NT = 2 while it fills half the slots; Q6_K (long K per superblock pass)
   // already from three eighths (3584 x 18944 at m = 512: 165 against 173 us;
   // Q4_K 14336 x 4096 at m = 128 stays faster with one tile, 46.6 against 50.9).
@@ -714,8 +791,8 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
   // captured graph has not been verified on the GPU, so captured launches
   // take the unsplit path.
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  HIP_TRY(hipStreamIsCapturing(s, &cs));
-  int splits = cs == hipStreamCaptureStatusNone ? env_int("COMBS_GEMM2_SPLIT", 0) : 1;
+  if (!g_plan) HIP_TRY(hipStreamIsCapturing(s, &cs));
+  int splits = cs == hipStreamCaptureStatusNone ? knobs().gemm2_split : 1;
   if (splits < 1) {
     splits = 1;
     while (gx * mblk * splits * 2 <= slots && a.units / (splits * 2) >= 3) splits *= 2;
@@ -727,7 +804,7 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
   const size_t sums_bytes = w->format != CQ_Q6_K ? (size_t)m * a.units * 32 : 0;
   const size_t part_bytes = splits > 1 ? (size_t)splits * m * w->n * 4 : 0;
   void* ws = nullptr;
-  if (sums_bytes + part_bytes) HIP_TRY(hipMallocAsync(&ws, sums_bytes + part_bytes, s));
+  if ((sums_bytes + part_bytes) && !g_plan) HIP_TRY(hipMallocAsync(&ws, sums_bytes + part_bytes, s));
   auto launch_all = [&]() -> hipError_t {
     hipError_t e;
     if (sums_bytes) {
@@ -735,19 +812,19 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
       const long long sums = m * a.units * 8;  // one thread per (row, superblock, sub-block)
       int M = a.M, K = a.K;
       void* sp[] = {(void*)&x, &ws, &M, &K};
-      e = hipModuleLaunchKernel(dm->xsums, (unsigned)((sums + 255) / 256), 1, 1, 256, 1, 1, 0, s, sp, nullptr);
+      e = klaunch(dm, dm->xsums, (unsigned)((sums + 255) / 256), 1, 1, 256, 0, s, sp);
       if (e != hipSuccess) return e;
     }
     if (part_bytes) a.part = (float*)((char*)ws + sums_bytes);
     void* params[] = {&a};
     hipFunction_t k = dm->gemm2[fi][nt - 1][mt / 8 - 1][yt];
-    e = hipModuleLaunchKernel(k, (unsigned)gx, (unsigned)mblk, (unsigned)splits, 64 * nw, 1, 1, 0, s, params, nullptr);
+    e = klaunch(dm, k, (unsigned)gx, (unsigned)mblk, (unsigned)splits, 64 * nw, 0, s, params);
     if (e != hipSuccess || !part_bytes) return e;
     long long mn = m * w->n;
     int n = (int)w->n;
     CqEpi ep = epi;
     void* rp[] = {&a.part, &y, &splits, &mn, &n, &ep};
-    return hipModuleLaunchKernel(dm->reduce[yt], (unsigned)((mn + 255) / 256), 1, 1, 256, 1, 1, 0, s, rp, nullptr);
+    return klaunch(dm, dm->reduce[yt], (unsigned)((mn + 255) / 256), 1, 1, 256, 0, s, rp);
   };
   const hipError_t e = launch_all();
   if (ws) HIP_TRY(hipFreeAsync(ws, s));
@@ -770,15 +847,14 @@ static cq_status launch_gemm(DeviceModule* dm, const cq_weight* w, const void* x
   a.K = (int)w->k;
   a.units = (int)(w->k / 256);
   a.epi = epi;
-  if (!xt && env_int("COMBS_GEMM_KERNEL", 2) == 2) return launch_gemm2(dm, w, x, m, y, yt, s, epi);
-  int nw = env_int("COMBS_GEMM_WAVES", 4);
+  if (!xt && knobs().gemm_kernel == 2) return launch_gemm2(dm, w, x, m, y, yt, s, epi);
+  int nw = knobs().gemm_waves;
   if (nw < 4 || nw > 8) nw = 4;  // the activation staging assumes >= 256 threads
   const int mb = xt ? 32 : 64;
   const long long gx = (w->n + 16 * nw - 1) / (16 * nw), gy = (m + mb - 1) / mb;
   if (gx > 0x7fffffffLL || gy > 65535) return fail(CQ_ERR_BAD_SHAPE, "grid too large");
   void* params[] = {&a};
-  HIP_TRY(hipModuleLaunchKernel(dm->gemm[fi][xt][yt], (unsigned)gx, (unsigned)gy, 1, 64 * nw, 1, 1, 0, s, params,
-                                nullptr));
+  HIP_TRY(klaunch(dm, dm->gemm[fi][xt][yt], (unsigned)gx, (unsigned)gy, 1, 64 * nw, 0, s, params));
   return CQ_OK;
 }
 
@@ -802,18 +878,18 @@ static cq_status matmul_impl(const cq_weight* w, const void* x, int x_dtype, int
   const bool kq = block_values(w->format) == 256;
   if (kq && (path == CQ_PATH_GEMM || (path == CQ_PATH_AUTO && m > 16)))
     return launch_gemm(dm, w, x, xt, m, y, yt, (hipStream_t)stream, epi);
-  if (m == 1 && !xt && path != CQ_PATH_GEMV && env_int("COMBS_GEMV1", 1)) {
+  if (m == 1 && !xt && path != CQ_PATH_GEMV && knobs().gemv1) {
     // quarter-superblock streaming kernel (cq_gemv2): COMBS_GEMV2=2 for
     // every K-quant, =1 for Q6_K, 0 (default) only where cq_gemv1 does not
     // fit (a K-quant weight whose bytes are not 16-byte aligned)
-    const int g2 = env_int("COMBS_GEMV2", 0);
+    const int g2 = knobs().gemv2;
     if (kq && (g2 == 2 || (g2 == 1 && w->format == CQ_Q6_K)) && gemv2_fits(w))
       return launch_gemv2(dm, w, x, y, yt, (hipStream_t)stream, epi);
     if (gemv1_fits(w)) return launch_gemv1(dm, w, x, y, yt, (hipStream_t)stream, epi);
-    if (gemv1k_fits(w) && env_int("COMBS_GEMV1K", 1)) return launch_gemv1k(dm, w, x, y, yt, (hipStream_t)stream, epi);
+    if (gemv1k_fits(w) && knobs().gemv1k) return launch_gemv1k(dm, w, x, y, yt, (hipStream_t)stream, epi);
     if (kq && w->k / 256 <= 64 && gemv2_fits(w)) return launch_gemv2(dm, w, x, y, yt, (hipStream_t)stream, epi);
   }
-  if (kq && !xt && m >= 2 && m <= 16 && env_int("COMBS_GEMVD", 1))
+  if (kq && !xt && m >= 2 && m <= 16 && knobs().gemvd)
     return launch_gemvd(dm, w, x, m, y, yt, (hipStream_t)stream, epi);
   return launch_gemv(dm, w, x, xt, m, y, yt, (hipStream_t)stream, epi);
 }
@@ -850,7 +926,7 @@ cq_status cq_matmul_gate_up(const cq_weight* gate, const cq_weight* up, const vo
   if (!x || !y) return fail(CQ_ERR_NULL, "NULL x or y");
   if (y_dtype != CQ_F16 && y_dtype != CQ_F32) return fail(CQ_ERR_BAD_DTYPE, "y_dtype %d", y_dtype);
   if (m == 1 && x_dtype == CQ_F16 && gate->format == up->format && gemv1_gated_fits(gate, up) &&
-      env_int("COMBS_GATEUP_FUSED", 1)) {
+      knobs().gateup_fused) {
     DeviceModule* dm;
     cq_status st = device_module(&dm);
     if (st != CQ_OK) return st;
@@ -887,9 +963,23 @@ cq_status cq_dequantize(int format, const void* device_bytes, size_t nbytes, int
   const long long blocks = (a.chunks + 255) / 256;
   if (blocks > 0x7fffffffLL) return fail(CQ_ERR_BAD_SHAPE, "tensor too large");
   void* params[] = {&a};
-  HIP_TRY(hipModuleLaunchKernel(dm->dequant[fmt_index(format)], (unsigned)blocks, 1, 1, 256, 1, 1, 0,
-                                (hipStream_t)stream, params, nullptr));
+  HIP_TRY(klaunch(dm, dm->dequant[fmt_index(format)], (unsigned)blocks, 1, 1, 256, 0, (hipStream_t)stream, params));
   return CQ_OK;
+}
+
+void cq_reload_options(void) { read_knobs(); (void)knobs(); }
+
+cq_status cq_matmul_kernels(const cq_weight* w, int x_dtype, int64_t m, int y_dtype, char* buf, size_t buflen) {
+  if (!buf || buflen == 0) return fail(CQ_ERR_NULL, "NULL or empty name buffer");
+  std::string names;
+  g_plan = &names;
+  // stand-in operand addresses: a dry run reads only their alignment
+  void* const fake = reinterpret_cast<void*>(static_cast<uintptr_t>(256));
+  const cq_status st = matmul_impl(w, fake, x_dtype, m, fake, y_dtype, CQ_PATH_AUTO, nullptr, CqEpi{});
+  g_plan = nullptr;
+  if (st != CQ_OK) return st;
+  snprintf(buf, buflen, "%s", names.c_str());
+  return names.size() < buflen ? CQ_OK : fail(CQ_ERR_BAD_SHAPE, "name buffer of %zu bytes too small", buflen);
 }
 
 const char* cq_last_error(void) { return g_err.c_str(); }

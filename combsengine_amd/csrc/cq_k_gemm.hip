@@ -1,0 +1,67 @@
+// Kernels of the library, compiled with hipcc --genco into one gfx950 code
+// object of four (cq_k_*.hip); the host library embeds all four and looks
+// each kernel up by its extern "C" name with hipModuleGetFunction.
+// This object: the prefill dequant-GEMMs (cq_gemm_*, cq_gemm2_*), the
+// activation sub-block sums of their min term (cq_xsums_f16) and the split-K
+// reduction (cq_splitk_reduce_*).
+#include "cq_gemm.h"
+#include "cq_gemm2.h"
+
+#define GEMM_KERNEL(NAME, FMT, XT, YT)                                               \
+  extern "C" __global__ void __launch_bounds__(512) NAME(const GemmArgs a) {         \
+    gemm_body<FMT, XT, YT>(a);                                                       \
+  }
+#define GEMM_FMT(fname, FMT)                          \
+  GEMM_KERNEL(cq_gemm_##fname##_xf16_yf32, FMT, 0, 0) \
+  GEMM_KERNEL(cq_gemm_##fname##_xf16_yf16, FMT, 0, 1) \
+  GEMM_KERNEL(cq_gemm_##fname##_xf32_yf32, FMT, 1, 0) \
+  GEMM_KERNEL(cq_gemm_##fname##_xf32_yf16, FMT, 1, 1)
+
+GEMM_FMT(q4_k, CQ_Q4_K)
+GEMM_FMT(q5_k, CQ_Q5_K)
+GEMM_FMT(q6_k, CQ_Q6_K)
+
+// MT = 8 tiles use 64-72 KB of LDS, so two 4-wave workgroups fill a compute
+// unit when each wave fits 256 registers (two waves per SIMD).  (One 8-wave
+// workgroup sharing the activation tile measured the same.)
+#define GEMM2_KERNEL_NW(NAME, FMT, YT, NT, MT, NW)                                                        \
+  extern "C" __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(MT == 8 ? 2 : 1))) \
+  NAME(const LtArgs a) {                                                                                    \
+    gemm2_body<FMT, YT, NT, MT, NW>(a);                                                                     \
+  }
+#define GEMM2_KERNEL(NAME, FMT, YT, NT, MT) GEMM2_KERNEL_NW(NAME, FMT, YT, NT, MT, 4)
+GEMM2_KERNEL(cq_gemm2_q4_k_n1_m8_yf32, CQ_Q4_K, 0, 1, 8)
+GEMM2_KERNEL(cq_gemm2_q4_k_n1_m8_yf16, CQ_Q4_K, 1, 1, 8)
+GEMM2_KERNEL(cq_gemm2_q4_k_n1_m16_yf32, CQ_Q4_K, 0, 1, 16)
+GEMM2_KERNEL(cq_gemm2_q4_k_n1_m16_yf16, CQ_Q4_K, 1, 1, 16)
+GEMM2_KERNEL(cq_gemm2_q4_k_n2_m8_yf32, CQ_Q4_K, 0, 2, 8)
+GEMM2_KERNEL(cq_gemm2_q4_k_n2_m8_yf16, CQ_Q4_K, 1, 2, 8)
+GEMM2_KERNEL(cq_gemm2_q4_k_n2_m16_yf32, CQ_Q4_K, 0, 2, 16)
+GEMM2_KERNEL(cq_gemm2_q4_k_n2_m16_yf16, CQ_Q4_K, 1, 2, 16)
+GEMM2_KERNEL(cq_gemm2_q5_k_n1_m8_yf32, CQ_Q5_K, 0, 1, 8)
+GEMM2_KERNEL(cq_gemm2_q5_k_n1_m8_yf16, CQ_Q5_K, 1, 1, 8)
+GEMM2_KERNEL(cq_gemm2_q5_k_n1_m16_yf32, CQ_Q5_K, 0, 1, 16)
+GEMM2_KERNEL(cq_gemm2_q5_k_n1_m16_yf16, CQ_Q5_K, 1, 1, 16)
+GEMM2_KERNEL(cq_gemm2_q5_k_n2_m8_yf32, CQ_Q5_K, 0, 2, 8)
+GEMM2_KERNEL(cq_gemm2_q5_k_n2_m8_yf16, CQ_Q5_K, 1, 2, 8)
+GEMM2_KERNEL(cq_gemm2_q5_k_n2_m16_yf32, CQ_Q5_K, 0, 2, 16)
+GEMM2_KERNEL(cq_gemm2_q5_k_n2_m16_yf16, CQ_Q5_K, 1, 2, 16)
+GEMM2_KERNEL(cq_gemm2_q6_k_n1_m8_yf32, CQ_Q6_K, 0, 1, 8)
+GEMM2_KERNEL(cq_gemm2_q6_k_n1_m8_yf16, CQ_Q6_K, 1, 1, 8)
+GEMM2_KERNEL(cq_gemm2_q6_k_n1_m16_yf32, CQ_Q6_K, 0, 1, 16)
+GEMM2_KERNEL(cq_gemm2_q6_k_n1_m16_yf16, CQ_Q6_K, 1, 1, 16)
+GEMM2_KERNEL(cq_gemm2_q6_k_n2_m8_yf32, CQ_Q6_K, 0, 2, 8)
+GEMM2_KERNEL(cq_gemm2_q6_k_n2_m8_yf16, CQ_Q6_K, 1, 2, 8)
+GEMM2_KERNEL(cq_gemm2_q6_k_n2_m16_yf32, CQ_Q6_K, 0, 2, 16)
+GEMM2_KERNEL(cq_gemm2_q6_k_n2_m16_yf16, CQ_Q6_K, 1, 2, 16)
+extern "C" __global__ void __launch_bounds__(256) cq_splitk_reduce_yf32(const float* part, void* y, int splits,
+                                                                       long long mn, int n, CqEpi epi) {
+  splitk_reduce_body<0>(part, y, splits, mn, n, epi);
+}
+extern "C" __global__ void __launch_bounds__(256) cq_splitk_reduce_yf16(const float* part, void* y, int splits,
+                                                                       long long mn, int n, CqEpi epi) {
+  splitk_reduce_body<1>(part, y, splits, mn, n, epi);
+}
+extern "C" __global__ void __launch_bounds__(256) cq_xsums_f16(const _Float16* x, _Float16* xs, int M, int K) {
+  xsums_body(x, xs, M, K);
+}

@@ -1,0 +1,24 @@
+// Kernels of the library, compiled with hipcc --genco into one gfx950 code
+// object of four (cq_k_*.hip); the host library embeds all four and looks
+// each kernel up by its extern "C" name with hipModuleGetFunction.
+// This object: the streaming quarter-superblock single-row GEMV cq_gemv2_*
+// (K-quants).
+#include "cq_gemv2.h"
+
+#ifndef CQ_GV2_DEPTH
+#define CQ_GV2_DEPTH 3
+#endif
+#define GV2_WAVES 8
+#define GEMV2_KERNEL(NAME, FMT, YT, EPI)                                                        \
+  extern "C" __global__ void __launch_bounds__(64 * GV2_WAVES) NAME(const Gv2Args a) {          \
+    gemv2_body<FMT, YT, GV2_WAVES, CQ_GV2_DEPTH, EPI>(a);                                       \
+  }
+#define GEMV2_FMT(fname, FMT)                          \
+  GEMV2_KERNEL(cq_gemv2_##fname##_yf32, FMT, 0, 0)     \
+  GEMV2_KERNEL(cq_gemv2_##fname##_yf16, FMT, 1, 0)     \
+  GEMV2_KERNEL(cq_gemv2_##fname##_yf32_epi, FMT, 0, 1) \
+  GEMV2_KERNEL(cq_gemv2_##fname##_yf16_epi, FMT, 1, 1)
+GEMV2_FMT(q4_k, CQ_Q4_K)
+GEMV2_FMT(q5_k, CQ_Q5_K)
+GEMV2_FMT(q6_k, CQ_Q6_K)
+

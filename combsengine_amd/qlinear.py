@@ -233,6 +233,15 @@ class QuantWeight:
         return y.cpu().numpy()
 
 
+def _kernel_input(x):
+    """x itself when the kernels take its dtype (fp16, fp32), else x in fp32."""
+    if str(x.dtype) in _XT:
+        return x
+    if not x.dtype.is_floating_point:
+        raise ModelError(f"unsupported activation dtype {x.dtype}")
+    return x.float()
+
+
 class QuantLinearOp:
     """trait QuantLinearOp (qlinear.rs:56-63) over a QuantWeight."""
 
@@ -240,18 +249,25 @@ class QuantLinearOp:
         self.w = weight
 
     def forward(self, x):
-        """x [batch, seq, k] (fp16 or fp32) -> [batch, seq, n_out], dtype of x
-        (the reference's output follows the input dtype, qlinear.rs:126-143)."""
+        """x [batch, seq, k] -> [batch, seq, n_out] in x's dtype (the
+        reference's output follows the input dtype, qlinear.rs:126-143).
+        fp16 and fp32 go to the kernels as they are; any other float dtype
+        (bf16) is cast to fp32 around the launch and the result cast back,
+        as the reference casts every non-f32 input (qlinear.rs:126-143)."""
         b, s, k = x.shape
-        y = self.w.matmul_device(x.reshape(b * s, k), out_dtype=x.dtype)
-        return y.reshape(b, s, self.w.n_out())
+        xk = _kernel_input(x)
+        y = self.w.matmul_device(xk.reshape(b * s, k), out_dtype=xk.dtype)
+        return y.reshape(b, s, self.w.n_out()).to(x.dtype)
 
     def forward_bias(self, x, bias):
         """forward(x) + bias broadcast over rows, one kernel (qlinear.rs:84-98)."""
         b, s, k = x.shape
-        y = _torch().empty((b * s, self.w.n_out()), dtype=x.dtype, device=x.device)
-        self.w.matmul_bias_into(x.reshape(b * s, k).contiguous(), bias.contiguous(), y)
-        return y.reshape(b, s, self.w.n_out())
+        xk = _kernel_input(x)
+        if bias is not None and str(bias.dtype) not in _XT:
+            bias = bias.float()
+        y = _torch().empty((b * s, self.w.n_out()), dtype=xk.dtype, device=x.device)
+        self.w.matmul_bias_into(xk.reshape(b * s, k).contiguous(), None if bias is None else bias.contiguous(), y)
+        return y.reshape(b, s, self.w.n_out()).to(x.dtype)
 
     def dims(self):
         return [self.w.n_out(), self.w.k()]
@@ -277,14 +293,14 @@ def gated_up(activation, gate: "QuantLinearOp", up: "QuantLinearOp", h):
     if gate.dims() != up.dims() or gate.dims()[1] != k:
         raise BadShape("gate/up", gate.dims(), up.dims())
     n = gate.dims()[0]
-    x = h.reshape(b * s, k).contiguous()
-    y = torch.empty((b * s, n), dtype=h.dtype, device=h.device)
+    x = _kernel_input(h).reshape(b * s, k).contiguous()
+    y = torch.empty((b * s, n), dtype=x.dtype, device=h.device)
     gate.w._io(x, y)
     xt, yt = _XT[str(x.dtype)], _XT[str(y.dtype)]
     st = L.lib().cq_matmul_gate_up(gate.w.handle, up.w.handle, x.data_ptr(), xt, b * s, int(Activation(activation)),
                                    y.data_ptr(), yt, _stream_ptr(x.device))
     _check(st, "cq_matmul_gate_up", "gate/up input", [b * s, k], list(x.shape))
-    return y.reshape(b, s, n)
+    return y.reshape(b, s, n).to(h.dtype)
 
 
 class Linear:

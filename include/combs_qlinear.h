@@ -147,6 +147,16 @@ cq_status cq_dequantize(int format, const void* device_bytes, size_t nbytes, int
 cq_status cq_quantize(int format, const float* src, int64_t rows, int64_t k, void* dst, size_t dst_bytes,
                       int threads);
 
+/* Diagnostics; no counterpart in the reference.
+ * cq_matmul_kernels: the comma-separated names of the kernels cq_matmul
+ * would launch for this weight, x_dtype, m and y_dtype (a dry run: nothing
+ * is launched or allocated; the device's code objects are loaded).
+ * cq_reload_options: re-read the COMBS_* tuning variables, which the library
+ * otherwise reads once, at its first launch; not to be called while another
+ * thread launches. */
+cq_status cq_matmul_kernels(const cq_weight* w, int x_dtype, int64_t m, int y_dtype, char* buf, size_t buflen);
+void cq_reload_options(void);
+
 /* Message of the calling thread's last error ("" if none). */
 const char* cq_last_error(void);
 

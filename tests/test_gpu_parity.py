@@ -391,10 +391,12 @@ def test_gemv_batched_gaussian_llama_shape(cuda, fmt, m):
     f64 = (torch.from_numpy(x).double() @ torch.from_numpy(wd).double().T).numpy()
     O.assert_close(got, f64, 1e-3, "f64")
     os.environ["COMBS_GEMVD"] = "0"
+    L.reload_options()
     try:
         old = _run(w, x, torch.float16, torch.float32)
     finally:
         os.environ.pop("COMBS_GEMVD")
+        L.reload_options()
     O.assert_close(got, old, 1e-3, "mfma gemv")
 
 

@@ -65,3 +65,11 @@ def test_quant_linear_matches_dense(cuda, fmt):
     q16, d16 = quant.forward(x.half(), bias), dense.forward(x.half(), bias)
     assert q16.dtype == torch.float16
     O.assert_close(q16.float().cpu().numpy(), d16.float().cpu().numpy(), 1e-2, "f16")
+    # bf16 activations: cast to fp32 around the launch, result cast back
+    # (the reference casts every non-f32 input, qlinear.rs:126-143)
+    xb = x.bfloat16()
+    qb = quant.forward(xb, bias)
+    assert qb.dtype == torch.bfloat16 and qb.shape == (2, 3, n)
+    db = dense.forward(xb.float(), bias).bfloat16()
+    O.assert_close(qb.float().cpu().numpy(), db.float().cpu().numpy(), 1e-2, "bf16")
+    assert op.forward(xb).dtype == torch.bfloat16

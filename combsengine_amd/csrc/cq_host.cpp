@@ -164,6 +164,14 @@ struct GvdArgs {
   int M, N, K, units;
   CqEpi epi;
 };
+struct GvrArgs {
+  const void* w;
+  const void* x;
+  void* y;
+  long long row_bytes;
+  int N, K, units, C, G, iters;
+  CqEpi epi;
+};
 struct DequantArgs {
   const void* w;
   float* out;
@@ -189,6 +197,7 @@ struct DeviceModule {
   hipFunction_t gemv1k[kNumFormats][2][2] = {};   // rows of 65-128 units, Q4_K / Q5_K / Q6_K / Q4_0 [format][y f16][epilogue]
   hipFunction_t gemv2[kNumFormats][2][2] = {};  // K-quants only     // [format][y f16]
   hipFunction_t gemvd[kNumFormats][3][2] = {};  // K-quants only: [format][NT 1, 2, 4][y f16]
+  hipFunction_t gemvr[2][4] = {};  // Q4_K rows split across lanes: [y f16][log2 activation pieces per thread]
   int cus = 0;                        // compute units of the device
 };
 DeviceModule g_dev[kMaxDevices];
@@ -219,7 +228,7 @@ void load_module(DeviceModule& d, int dev) {
   // last-error state for the caller's next check to find.
   auto get = [&d](hipFunction_t* f, const char* nm) {
     const std::string n(nm);
-    const int mi = n.rfind("cq_gemv1", 0) == 0 ? 1 : n.rfind("cq_gemv2", 0) == 0 ? 2
+    const int mi = (n.rfind("cq_gemv1", 0) == 0 || n.rfind("cq_gemvr", 0) == 0) ? 1 : n.rfind("cq_gemv2", 0) == 0 ? 2
                    : (n.rfind("cq_gemm", 0) == 0 || n.rfind("cq_xsums", 0) == 0 || n.rfind("cq_splitk", 0) == 0) ? 3
                    : 0;
     const hipError_t e = hipModuleGetFunction(f, d.mods[mi], nm);
@@ -303,6 +312,14 @@ void load_module(DeviceModule& d, int dev) {
         }
       }
   }
+  for (int yt = 0; yt < 2; yt++)
+    for (int xl = 0; xl < 4; xl++) {
+      snprintf(name, sizeof name, "cq_gemvr_q4_k_y%s_x%d", yt ? "f16" : "f32", 1 << xl);
+      if (get(&d.gemvr[yt][xl], name) != hipSuccess) {
+        d.err = std::string("missing kernel ") + name;
+        return;
+      }
+    }
   if (get(&d.reduce[0], "cq_splitk_reduce_yf32") != hipSuccess ||
       get(&d.reduce[1], "cq_splitk_reduce_yf16") != hipSuccess) {
     d.err = "missing kernel cq_splitk_reduce_*";
@@ -335,7 +352,7 @@ constexpr int kUnset = -1000000;
 struct Knobs {
   int gemv_waves, gemv1, gemv1k, gemv1_grid, gemv1_i8, gemv1_prefetch2, gemv1_span, gemv1_spread,
       gemv1_wave_major, gemv2, gemv2_wpc, gemvd, gvd_nt, gvd_waves, gemm_kernel, gemm_waves, gemm2_mt,
-      gemm2_nt, gemm2_split, gateup_fused;
+      gemm2_nt, gemm2_split, gateup_fused, gemvr;
 };
 Knobs g_knobs;
 std::once_flag g_knobs_once;
@@ -366,6 +383,7 @@ void read_knobs() {
   k.gemm2_nt = env_int("COMBS_GEMM2_NT", 0);
   k.gemm2_split = env_int("COMBS_GEMM2_SPLIT", 0);
   k.gateup_fused = env_int("COMBS_GATEUP_FUSED", 1);
+  k.gemvr = env_int("COMBS_GEMVR", 1);
   g_knobs = k;
 }
 const Knobs& knobs() {
@@ -648,6 +666,48 @@ static cq_status launch_gemv1k(DeviceModule* dm, const cq_weight* w, const void*
   HIP_TRY(klaunch(dm, dm->gemv1k[fi][yt][ep], (unsigned)grid, 1, 1, 64 * 4, 0, s, params));
   return CQ_OK;
 }
+// Row-split single-row decode (cq_gemvr_*, Q4_K): row groups of C =
+// ceil(4 units / 64) waves, 8 / C row groups per workgroup of up to 8
+// waves, one workgroup per compute unit, each wave with four rows of loads
+// in flight; the activation row is staged by every thread in 1, 2, 4 or 8
+// 16-byte pieces.  The default for Q4_K rows whose quarters do not fill a
+// whole number of waves (units % 16 != 0), where cq_gemv1 leaves lanes
+// idle: Qwen2.5-7B 3584 x 3584 5.75 against 6.05 us, 18944 x 3584 11.9
+// against 13.7, 3584 x 18944 13.9 against 14.5 (cq_gemv1k); on the
+// Llama-3-8B shapes (16 and 56 units) cq_gemv1 measured faster (9.7 against
+// 10.2 us at 14336 x 4096).  COMBS_GEMVR=0 never, 2 always where it fits.
+constexpr int kGvrMaxK = 32768;
+constexpr int kGvrWaves = 8;
+static bool gemvr_fits(const cq_weight* w) {
+  return w->format == CQ_Q4_K && w->k % 256 == 0 && w->k <= kGvrMaxK;
+}
+static bool gemvr_default(const cq_weight* w) { return (w->k / 256) % 16 != 0; }
+static cq_status launch_gemvr(DeviceModule* dm, const cq_weight* w, const void* x, void* y, int yt, hipStream_t s,
+                              const CqEpi& epi) {
+  GvrArgs a{};
+  a.w = w->dev;
+  a.x = x;
+  a.y = y;
+  a.row_bytes = (long long)(w->nbytes / (size_t)w->n);
+  a.N = (int)w->n;
+  a.K = (int)w->k;
+  a.units = (int)(w->k / 256);
+  a.C = (4 * a.units + 63) / 64;
+  a.G = kGvrWaves / a.C;
+  a.epi = epi;
+  const int threads = 64 * a.C * a.G;
+  const int need = (a.K / 8 + threads - 1) / threads;
+  int xl = 0;
+  while ((1 << xl) < need) xl++;
+  if (xl > 3) return fail(CQ_ERR_BAD_SHAPE, "gemvr: K=%d out of range", a.K);
+  const long long groups_needed = (w->n + a.G - 1) / a.G;
+  const int grid = (int)(groups_needed < dm->cus ? groups_needed : dm->cus);
+  const long long total = (long long)grid * a.G;
+  a.iters = (int)((w->n + total - 1) / total);
+  void* params[] = {&a};
+  HIP_TRY(klaunch(dm, dm->gemvr[yt][xl], (unsigned)grid, 1, 1, threads, 0, s, params));
+  return CQ_OK;
+}
 // The one-launch gated gate/up: a task needs >= 2 rows (K / 256 <= 32),
 // and both weights must suit the span loads.
 static bool gemv1_gated_fits(const cq_weight* gate, const cq_weight* up) {
@@ -885,6 +945,8 @@ static cq_status matmul_impl(const cq_weight* w, const void* x, int x_dtype, int
     const int g2 = knobs().gemv2;
     if (kq && (g2 == 2 || (g2 == 1 && w->format == CQ_Q6_K)) && gemv2_fits(w))
       return launch_gemv2(dm, w, x, y, yt, (hipStream_t)stream, epi);
+    if (gemvr_fits(w) && !epi.bias && !epi.aux && (knobs().gemvr == 2 || (knobs().gemvr == 1 && gemvr_default(w))))
+      return launch_gemvr(dm, w, x, y, yt, (hipStream_t)stream, epi);
     if (gemv1_fits(w)) return launch_gemv1(dm, w, x, y, yt, (hipStream_t)stream, epi);
     if (gemv1k_fits(w) && knobs().gemv1k) return launch_gemv1k(dm, w, x, y, yt, (hipStream_t)stream, epi);
     if (kq && w->k / 256 <= 64 && gemv2_fits(w)) return launch_gemv2(dm, w, x, y, yt, (hipStream_t)stream, epi);

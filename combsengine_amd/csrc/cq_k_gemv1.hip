@@ -4,6 +4,7 @@
 // This object: the single-row decode GEMVs cq_gemv1_* (fp16-register and
 // int8 paths, gated gate/up) and cq_gemv1k_* (rows of 65-128 units).
 #include "cq_gemv1.h"
+#include "cq_gemvr.h"
 
 #define GEMV1_KERNEL(NAME, FMT, YT, EPI)                                                \
   extern "C" __global__ void __launch_bounds__((64 * gv1_kernel_waves<FMT, EPI>())) NAME(const Gv1Args a) { \
@@ -56,3 +57,18 @@ GEMV1K_FMT(q5_k, CQ_Q5_K)
 GEMV1K_FMT(q6_k, CQ_Q6_K)
 GEMV1K_FMT(q4_0, CQ_Q4_0)
 
+
+// Single-row decode with rows split across a wave's lanes (cq_gemvr.h):
+// [y dtype] x [activation pieces per thread 1, 2, 4, 8]; four rows of loads
+// in flight per wave (eight measured slower at every shape tried).
+#define GEMVR_KERNEL(NAME, YT, XR)                                                               \
+  extern "C" __global__ void __launch_bounds__(64 * GVR_MAXW) NAME(const GvrArgs a) {            \
+    gvr_q4k_body<YT, XR, 4>(a);                                                                  \
+  }
+#define GEMVR_Y(YN, YT)                              \
+  GEMVR_KERNEL(cq_gemvr_q4_k_##YN##_x1, YT, 1)       \
+  GEMVR_KERNEL(cq_gemvr_q4_k_##YN##_x2, YT, 2)       \
+  GEMVR_KERNEL(cq_gemvr_q4_k_##YN##_x4, YT, 4)       \
+  GEMVR_KERNEL(cq_gemvr_q4_k_##YN##_x8, YT, 8)
+GEMVR_Y(yf32, 0)
+GEMVR_Y(yf16, 1)

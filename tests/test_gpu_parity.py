@@ -163,7 +163,7 @@ KQ = [QuantFormat.Q4K, QuantFormat.Q5K, QuantFormat.Q6K]
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("n,k", [(300, 4096), (35, 512), (97, 3584), (50, 5120), (70, 14336), (130, 16384), (1, 256),
                                  (2053, 1024), (3000, 768), (9, 4352)])
-@pytest.mark.parametrize("kernel", ["gemv2", "gemv1", "gemv1reg", "gemv1i8", "gemv1packed", "mfma"])
+@pytest.mark.parametrize("kernel", ["gemv2", "gemv1", "gemv1reg", "gemv1i8", "gemv1packed", "mfma", "gemvr"])
 def test_gemv_single_row(cuda, monkeypatch, fmt, n, k, kernel):
     """m = 1 fp16 decode through each single-row kernel: the streaming
     quarter-superblock kernel (gemv2, K-quants: steps of 16 superblocks, R =
@@ -178,6 +178,9 @@ def test_gemv_single_row(cuda, monkeypatch, fmt, n, k, kernel):
     import torch
     if kernel == "gemv2" and fmt in LEGACY:
         pytest.skip("gemv2 serves the K-quants")
+    if kernel == "gemvr" and fmt != QuantFormat.Q4K:
+        pytest.skip("the row-split kernel serves Q4_K")
+    monkeypatch.setenv("COMBS_GEMVR", "2" if kernel == "gemvr" else "0")
     monkeypatch.setenv("COMBS_GEMV1", "0" if kernel == "mfma" else "1")
     monkeypatch.setenv("COMBS_GEMV2", "2" if kernel == "gemv2" else "0")
     monkeypatch.setenv("COMBS_GEMV1_I8", {"gemv1reg": "0", "gemv1i8": "2"}.get(kernel, "1"))
@@ -403,7 +406,7 @@ def test_gemv_batched_gaussian_llama_shape(cuda, fmt, m):
 @pytest.mark.parametrize("fmt", [QuantFormat.Q4K, QuantFormat.Q5K, QuantFormat.Q6K, QuantFormat.Q4_0, QuantFormat.Q8_0])
 @pytest.mark.parametrize("n,k", [(300, 18944), (67, 16640), (40, 33024), (3, 18944), (37, 27136), (513, 32768),
                                  (1029, 17152)])
-@pytest.mark.parametrize("kernel", ["gemv1k", "mfma"])
+@pytest.mark.parametrize("kernel", ["gemv1k", "mfma", "gemvr"])
 def test_gemv_single_row_long_k(cuda, monkeypatch, fmt, n, k, kernel):
     """m = 1 with K above the single-row kernels' 16384 (a Qwen2.5-7B down
     projection is 18944 wide): rows of 65 to 128 units (106 for Q6_K) on the
@@ -412,7 +415,10 @@ def test_gemv_single_row_long_k(cuda, monkeypatch, fmt, n, k, kernel):
     idle), the rest and COMBS_GEMV1K=0 on the 16-row MFMA GEMV; fp32 and
     fp16 y, checked against the oracle and for bit-identical repeats."""
     import torch
+    if kernel == "gemvr" and (fmt != QuantFormat.Q4K or k > 32768):
+        pytest.skip("the row-split kernel serves Q4_K up to K = 32768")
     monkeypatch.setenv("COMBS_GEMV1K", "1" if kernel == "gemv1k" else "0")
+    monkeypatch.setenv("COMBS_GEMVR", "2" if kernel == "gemvr" else "0")
     data = synth(fmt, n, k)
     wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
     w = QuantWeight.from_gguf_bytes(fmt, data, n, k)

@@ -61,6 +61,7 @@ def test_gemv1_many_tasks_per_wave(cuda, monkeypatch, fmt, n, k):
     # Q4_0 / Q8_0 weights take by default differ in the last bits): the
     # fp16-register kernels where they serve the format
     monkeypatch.setenv("COMBS_GEMV1_I8", "0")
+    monkeypatch.setenv("COMBS_GEMVR", "0")  # cq_gemv1 on every grid
     for grid in ("1", "2", "3", "default"):
         if grid == "default":
             monkeypatch.delenv("COMBS_GEMV1_GRID", raising=False)

@@ -3,9 +3,11 @@
 1. hipcc --genco compiles each csrc/cq_k_*.hip (the device code, split in
    four translation units that compile in parallel) into a gfx950 code
    object, lib/cq_k_*.hsaco.
-2. g++ compiles the host side (C ABI, module loading, quantisers) into
-   lib/libcombs_qlinear.so, embedding the code objects with .incbin, and
-   links the HIP runtime (libamdhip64).
+2. hipcc compiles csrc/cq_scratch.hip (the no-allocation entry point's
+   device scratch array and its address lookup) into lib/cq_scratch.o.
+3. g++ compiles the host side (C ABI, module loading, quantisers) into
+   lib/libcombs_qlinear.so, embedding the code objects with .incbin, links
+   cq_scratch.o and the HIP runtime (libamdhip64).
 
 The .so is self-contained: it loads its kernels with hipModuleLoadData at
 first use on each device.
@@ -61,9 +63,13 @@ def build(verbose: bool = False) -> str:
     stale = os.path.join(LIBDIR, "cq_gfx950.hsaco")  # the former single code object
     if os.path.exists(stale):
         os.remove(stale)
+    # the no-allocation entry point's scratch array (host + device object)
+    scratch_o = os.path.join(LIBDIR, "cq_scratch.o")
+    _run([os.path.join(ROCM, "bin", "hipcc"), "-c", "-fPIC", *HIPCC_FLAGS, os.path.join(CSRC, "cq_scratch.hip"),
+          "-o", scratch_o], verbose)
     _run(["g++", "-O2", "-fPIC", "-shared", "-std=c++17", "-fopenmp", "-Wall",
           "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", f'-DCQ_HSACO_DIR="{LIBDIR}"',
-          os.path.join(CSRC, "cq_host.cpp"), os.path.join(CSRC, "cq_quantize.cpp"),
+          os.path.join(CSRC, "cq_host.cpp"), os.path.join(CSRC, "cq_quantize.cpp"), scratch_o,
           f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib", "-o", SO], verbose)
     return SO
 

@@ -38,6 +38,10 @@ CQ_EMBED(gemv1)
 CQ_EMBED(gemv2)
 CQ_EMBED(gemm)
 
+// cq_scratch.hip: device address of the fixed scratch array on the current
+// device (looked up once per device).
+extern "C" hipError_t cq_scratch_device_ptr(void** out, size_t* bytes);
+
 namespace {
 
 thread_local std::string g_err;
@@ -390,6 +394,15 @@ const Knobs& knobs() {
   std::call_once(g_knobs_once, read_knobs);
   return g_knobs;
 }
+
+// The no-allocation entry point (cq_matmul_noalloc): while set, the prefill
+// GEMM takes its scratch from this fixed device buffer instead of
+// hipMallocAsync.
+struct FixedScratch {
+  void* ptr;
+  size_t bytes;
+};
+thread_local const FixedScratch* g_fixed = nullptr;
 
 // Dry runs (cq_matmul_kernels): while set, launches record the kernel name
 // instead of running and no scratch memory is allocated.
@@ -858,13 +871,28 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
     while (gx * mblk * splits * 2 <= slots && a.units / (splits * 2) >= 3) splits *= 2;
   }
   if (splits > a.units) splits = a.units;
+  // Scratch: activation sums (Q4_K/Q5_K), then split partials; stream-ordered
+  // (hipMallocAsync), or the fixed buffer of cq_matmul_noalloc, where the
+  // split count halves until the partials fit.
+  const size_t sums_bytes = w->format != CQ_Q6_K ? (size_t)m * a.units * 32 : 0;
+  auto part_size = [&](int sp) -> size_t {
+    const int us = (a.units + sp - 1) / sp;
+    const int n_sp = (a.units + us - 1) / us;
+    return n_sp > 1 ? (size_t)n_sp * m * w->n * 4 : 0;
+  };
+  if (g_fixed) {
+    if (sums_bytes > g_fixed->bytes)
+      return fail(CQ_ERR_BAD_SHAPE,
+                  "no-alloc prefill: activation sums of %lld x %lld need %zu bytes, the fixed scratch holds %zu",
+                  (long long)m, (long long)w->k, sums_bytes, g_fixed->bytes);
+    while (splits > 1 && sums_bytes + part_size(splits) > g_fixed->bytes) splits /= 2;
+  }
   a.usplit = (a.units + splits - 1) / splits;
   splits = (a.units + a.usplit - 1) / a.usplit;
-  // Stream-ordered scratch: activation sums (Q4_K/Q5_K), then split partials.
-  const size_t sums_bytes = w->format != CQ_Q6_K ? (size_t)m * a.units * 32 : 0;
   const size_t part_bytes = splits > 1 ? (size_t)splits * m * w->n * 4 : 0;
   void* ws = nullptr;
-  if ((sums_bytes + part_bytes) && !g_plan) HIP_TRY(hipMallocAsync(&ws, sums_bytes + part_bytes, s));
+  if (g_fixed) ws = g_fixed->ptr;
+  else if ((sums_bytes + part_bytes) && !g_plan) HIP_TRY(hipMallocAsync(&ws, sums_bytes + part_bytes, s));
   auto launch_all = [&]() -> hipError_t {
     hipError_t e;
     if (sums_bytes) {
@@ -887,7 +915,7 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
     return klaunch(dm, dm->reduce[yt], (unsigned)((mn + 255) / 256), 1, 1, 256, 0, s, rp);
   };
   const hipError_t e = launch_all();
-  if (ws) HIP_TRY(hipFreeAsync(ws, s));
+  if (ws && !g_fixed) HIP_TRY(hipFreeAsync(ws, s));
   if (e != hipSuccess) return fail(CQ_ERR_HIP, "prefill GEMM launch: %s", hipGetErrorString(e));
   return CQ_OK;
 }
@@ -1027,6 +1055,30 @@ cq_status cq_dequantize(int format, const void* device_bytes, size_t nbytes, int
   void* params[] = {&a};
   HIP_TRY(klaunch(dm, dm->dequant[fmt_index(format)], (unsigned)blocks, 1, 1, 256, 0, (hipStream_t)stream, params));
   return CQ_OK;
+}
+
+cq_status cq_matmul_noalloc(const cq_weight* w, const void* x, int x_dtype, int64_t m, void* y, int y_dtype,
+                            void* stream) {
+  DeviceModule* dm;
+  cq_status st = device_module(&dm);
+  if (st != CQ_OK) return st;
+  FixedScratch fs{nullptr, 0};
+  const hipError_t e = cq_scratch_device_ptr(&fs.ptr, &fs.bytes);
+  if (e != hipSuccess) return fail(CQ_ERR_HIP, "scratch address: %s", hipGetErrorString(e));
+  g_fixed = &fs;
+  st = matmul_impl(w, x, x_dtype, m, y, y_dtype, CQ_PATH_AUTO, stream, CqEpi{});
+  g_fixed = nullptr;
+  return st;
+}
+
+cq_status cq_device_init(void) {
+  DeviceModule* dm;
+  cq_status st = device_module(&dm);
+  if (st != CQ_OK) return st;
+  void* p = nullptr;
+  size_t b = 0;
+  const hipError_t e = cq_scratch_device_ptr(&p, &b);
+  return e == hipSuccess ? CQ_OK : fail(CQ_ERR_HIP, "scratch address: %s", hipGetErrorString(e));
 }
 
 void cq_reload_options(void) { read_knobs(); (void)knobs(); }

@@ -147,6 +147,23 @@ cq_status cq_dequantize(int format, const void* device_bytes, size_t nbytes, int
 cq_status cq_quantize(int format, const float* src, int64_t rows, int64_t k, void* dst, size_t dst_bytes,
                       int threads);
 
+/* cq_matmul that allocates nothing.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, kernels and results as cq_matmul; where cq_matmul takes
+ * stream-ordered scratch (the prefill GEMM's activation sums and split-K
+ * partials) this uses a fixed 32 MiB device array that the library holds
+ * on each device until the process ends, shrinking the K split until the
+ * partials fit; a prefill whose activation sums alone (m * K / 8 bytes for
+ * Q4_K / Q5_K) exceed it returns CQ_ERR_BAD_SHAPE.  Every call on a device
+ * shares that device's array (nothing in it needs to start zeroed), so calls
+ * that overlap on one device, on different streams or threads, race.  The
+ * first call on a device loads the code objects and looks up the array's
+ * address; cq_device_init does that ahead of time. */
+cq_status cq_matmul_noalloc(const cq_weight* w, const void* x, int x_dtype, int64_t m, void* y, int y_dtype,
+                            void* stream);
+cq_status cq_device_init(void);
+
 /* Diagnostics; no counterpart in the reference.
  * cq_matmul_kernels: the comma-separated names of the kernels cq_matmul
  * would launch for this weight, x_dtype, m and y_dtype (a dry run: nothing

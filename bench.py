@@ -1,26 +1,31 @@
 """Benchmark of the fused GGUF dequant-matmul on one MI355X.
 
 Headline (BASELINE.json metric "Q4_K decode GEMV HBM GB/s (% of peak)"):
-one step = one decode token's Q4_K projections at Llama-3-8B shapes, batch 1:
-a [14336 x 4096] (gate/up) and a [4096 x 14336] (down) GEMV, the two K-quant
-projection shapes of BASELINE config 3; x fp16 N(0, 1), y fp32.  Weights are
+one step = one decode token's Q4_K projections at the two Llama-3-8B
+projection shapes of BASELINE config 3, batch 1: a [14336 x 4096] (gate/up)
+and a [4096 x 14336] (down) GEMV; x fp16 N(0, 1), y fp32.  Weights are
 N(0, 0.02) quantised to Q4_K from a seed and replicated into a pool of
 >= 1.25 GiB of distinct device buffers that the steps rotate through, so each
-launch streams its weight from HBM rather than the 256 MB Infinity Cache.
+launch streams its weight from HBM rather than the 256 MB Infinity Cache; the
+timed steps start on buffers the warmup did not touch.
 
 The K timed steps are captured once into a HIP graph (torch.cuda.CUDAGraph
 over the library's hipModuleLaunchKernel calls) and replayed, so the number
 measures the kernels back to back rather than Python's launch overhead.
 
 value = algorithmic bytes (GGUF-native weight bytes + x + y) of K steps
-        / device time of the K steps (HIP events around the graph replay).
+        / device time of the K steps (HIP events around one graph replay).
+The same graph is replayed until at least 100 launches have been timed, and
+the median / p10 / p90 of the per-step time over those replays are reported.
 
-Also reported: the roofline of the dominant kernel (cq_gemv1_q4_k_yf32, the
-single-row decode GEMV)
-from graphs of single-shape launches, prefill dequant-GEMM TFLOP/s (config 4,
-the faster of eager launches, which may split K, and a captured graph),
-lm_head Q6_K and batch 4/16, and the reference CPU path (dequantise once,
-dense f32 GEMV per call) timed on this host as cpu_baseline.
+Also reported: the roofline of the dominant kernel (median per-launch time
+of >= 100 graph-replayed launches of one shape), empty-launch overhead,
+decode tokens/s of a whole Llama-3-8B token's projection set (32 layers + the
+Q6_K lm_head, one captured graph), prefill dequant-GEMM TFLOP/s (config 4,
+eager and graph-captured separately), lm_head Q6_K, batch 4/16, BASELINE
+configs 2/3/5, and the reference CPU path timed on this host: cpu_baseline
+on a bounded sample of the headline workload, and BASELINE config 1 (Q8_0
+[1536 x 576], fp32 x) with 1 thread and all cores.
 """
 import argparse
 import json
@@ -32,33 +37,42 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
-HEADLINE_KERNEL = "cq_gemv1_q4_k_yf32"  # what cq_matmul launches for m = 1, fp16 x, Q4_K
+HEADLINE_KERNEL = "cq_gemv1_q4_k_yf32"  # what cq_matmul launches for m = 1, fp16 x, Q4_K [14336 x 4096]
 FP16_PEAK_TFLOPS = 2500.0
+MIN_LAUNCHES = 100
 
 
 def algo_bytes(wbytes, m, k, n, xbytes=2, ybytes=4):
     return wbytes + m * k * xbytes + m * n * ybytes
 
 
+def quantized_weight(fmt, n, k, seed):
+    """N(0, 0.02) [n x k] from a seeded generator (torch, on the GPU: fast at
+    lm_head size), quantised on the host; returns the block stream (uint8)."""
+    import numpy as np
+    import torch
+    from combsengine_amd import quantize
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    w = (torch.randn((n, k), generator=g, device="cuda", dtype=torch.float32) * 0.02).cpu().numpy()
+    return np.frombuffer(quantize(fmt, w), np.uint8)
+
+
 def make_pool(fmt, n, k, pool_bytes, seed, count=None):
     """One seeded quantised weight, replicated into distinct device buffers
     (`count` of them, or as many as fit in `pool_bytes`)."""
-    import numpy as np
     import torch
-    from combsengine_amd import QuantWeight, quantize
-    rng = np.random.default_rng(seed)
-    data = np.frombuffer(quantize(fmt, rng.normal(0, 0.02, (n, k)).astype(np.float32)), np.uint8)
+    from combsengine_amd import QuantWeight
+    data = quantized_weight(fmt, n, k, seed)
     base = torch.from_numpy(data.copy()).cuda()
     count = count or max(1, int(pool_bytes // data.size))
     pool = [QuantWeight.from_device(fmt, base if i == 0 else base.clone(), n, k) for i in range(count)]
     return pool, data
 
 
-def graph_time_us(launch, count, reps=3):
-    """Capture `count` launches (launch(i)) in one HIP graph; return the
-    device time per launch (us), best of `reps` replays."""
+def capture(launch, count):
+    """Capture launch(0) .. launch(count - 1) into one HIP graph."""
     import torch
-    launch(0)  # make sure the library and modules are loaded outside capture
+    launch(0)  # library and modules loaded outside the capture
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
@@ -70,27 +84,50 @@ def graph_time_us(launch, count, reps=3):
     torch.cuda.current_stream().wait_stream(s)
     g.replay()
     torch.cuda.synchronize()
-    best = None
+    return g
+
+
+def replay_times(g, count, reps):
+    """Device time per launch (us) of each of `reps` replays of graph g
+    (which holds `count` launches), HIP events around each replay."""
+    import torch
+    out = []
     for _ in range(reps):
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
         g.replay()
         b.record()
         torch.cuda.synchronize()
-        t = a.elapsed_time(b) * 1e3 / count
-        best = t if best is None else min(best, t)
-    return best, g
+        out.append(a.elapsed_time(b) * 1e3 / count)
+    return out
 
 
-def eager_time_us(launch, count, reps=3):
-    """Device time per launch (us) of `count` eager launches on the current
-    stream (HIP events around them), best of `reps`.  Used for the prefill
-    GEMMs: each launch runs 30-600 us, so host launch overhead is hidden,
-    and the eager path may split K (captured launches do not)."""
+def stats(v):
+    import numpy as np
+    v = np.asarray(v, np.float64)
+    return {"median": round(float(np.median(v)), 3), "p10": round(float(np.percentile(v, 10)), 3),
+            "p90": round(float(np.percentile(v, 90)), 3), "n": int(v.size)}
+
+
+def graph_time_us(launch, count, reps=None):
+    """Median device time per launch (us) over replays of a graph of `count`
+    launches, enough replays for >= MIN_LAUNCHES timed launches (at least 5);
+    returns (median, stats)."""
+    g = capture(launch, count)
+    reps = reps or max(5, -(-MIN_LAUNCHES // count))
+    st = stats(replay_times(g, count, reps))
+    return st["median"], st
+
+
+def eager_time_us(launch, count, reps=None):
+    """Median device time per launch (us) of bursts of `count` eager launches
+    on the current stream (HIP events around each burst), enough bursts for
+    >= MIN_LAUNCHES launches; returns (median, stats)."""
     import torch
     launch(0)
     torch.cuda.synchronize()
-    best = None
+    reps = reps or max(5, -(-MIN_LAUNCHES // count))
+    out = []
     for _ in range(reps):
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
@@ -98,125 +135,9 @@ def eager_time_us(launch, count, reps=3):
             launch(i)
         b.record()
         torch.cuda.synchronize()
-        t = a.elapsed_time(b) * 1e3 / count
-        best = t if best is None else min(best, t)
-    return best
-
-
-def load_traffic():
-    p = os.path.join(ROOT, "profiles", "traffic.json")
-    if os.path.exists(p):
-        with open(p) as f:
-            return json.load(f)
-    return {}
-
-
-def cpu_baseline(seconds=6.0):
-    """Reference CPU path (dequantise at load, dense f32 GEMV per call) on the
-    headline gate shape, 1 thread (matrixmultiply without threading) and all
-    cores; reported in the same GB/s metric as the GPU."""
-    import numpy as np
-    import oracle as O
-    from combsengine_amd import QuantFormat, quantize
-    n, k = 14336, 4096
-    rng = np.random.default_rng(7)
-    data = np.frombuffer(quantize(QuantFormat.Q4K, rng.normal(0, 0.02, (n, k)).astype(np.float32)), np.uint8)
-    t0 = time.perf_counter()
-    w = O.dequant(O.Q4_K, data, n * k, threads=1).reshape(n, k)
-    t_deq = time.perf_counter() - t0
-    x = rng.normal(0, 1, (1, k)).astype(np.float16).astype(np.float32)
-    res = {}
-    for threads in (1, os.cpu_count() or 1):
-        calls, t0 = 0, time.perf_counter()
-        while True:
-            O.dense_gemm(x, w, threads)
-            calls += 1
-            el = time.perf_counter() - t0
-            if el > seconds / 2:
-                break
-        res[threads] = (calls, el)
-    per = algo_bytes(data.size, 1, k, n)
-    c1, e1 = res[1]
-    call_max = max(res)
-    cm, em = res[call_max]
-    return {
-        "value": round(per * c1 / e1 / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-        "sample": f"Q4_K [{n}x{k}] m=1: dequantise once ({t_deq:.2f} s, 1 thread), then {c1} dense f32 GEMV "
-                  f"calls in {e1:.1f} s on 1 thread (oracle restatement of llama.rs:81-97 -> sgemm)",
-        "all_cores": {"value": round(per * cm / em / 1e9, 3), "cores": call_max, "calls": cm},
-        "dequant_s": round(t_deq, 3), "ms_per_call_1t": round(e1 / c1 * 1e3, 3),
-    }
-
-
-def secondary(dev):
-    """Prefill dequant-GEMM (config 4: the faster of eager launches through
-    fast_launcher, which may split K, and a captured graph, which does not), lm_head Q6_K and batch
-    4/16 GEMV (captured graphs)."""
-    import numpy as np
-    import torch
-    from combsengine_amd import QuantFormat
-    out = {}
-    rng = np.random.default_rng(9)
-    # prefill: M in {128, 512, 2048} x Q4_K [14336 x 4096] and Q6_K [4096 x 14336], fp16 out
-    for fmt, n, k in ((QuantFormat.Q4K, 14336, 4096), (QuantFormat.Q6K, 4096, 14336)):
-        pool, data = make_pool(fmt, n, k, 0.3 * (1 << 30), seed=300 + int(fmt))
-        for m in (128, 512, 2048):
-            x = torch.from_numpy(rng.normal(0, 1, (m, k)).astype(np.float16)).to(dev)
-            y = torch.empty((m, n), dtype=torch.float16, device=dev)
-            launch = lambda i: pool[i % len(pool)].matmul_into(x, y)  # noqa: E731
-            cnt = 40 if m < 2048 else 16
-            # eager: the library call with its arguments resolved once (no
-            # Python-side checks per launch), as in the config 2/3/5 bursts
-            us_e = eager_time_us(fast_launcher(pool, x, y), cnt)
-            us_g, _ = graph_time_us(launch, cnt)
-            us = min(us_e, us_g)
-            fl = 2.0 * m * n * k
-            out[f"prefill_{fmt.name}_{n}x{k}_m{m}"] = {"us": round(us, 2), "TFLOPs": round(fl / us / 1e6, 1),
-                                                      "frac_fp16_peak": round(fl / us / 1e6 / FP16_PEAK_TFLOPS, 4),
-                                                      "us_eager": round(us_e, 2), "us_graph": round(us_g, 2)}
-        del pool
-    # lm_head Q6_K [128256 x 4096] (431 MB: larger than the Infinity Cache)
-    pool, data = make_pool(QuantFormat.Q6K, 128256, 4096, 2 * 431e6, seed=77)
-    x = torch.from_numpy(rng.normal(0, 1, (1, 4096)).astype(np.float16)).to(dev)
-    y = torch.empty((1, 128256), dtype=torch.float32, device=dev)
-    us, _ = graph_time_us(lambda i: pool[i % len(pool)].matmul_into(x, y), 8)
-    b = algo_bytes(data.size, 1, 4096, 128256)
-    out["lm_head_q6_k_m1"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1)}
-    del pool
-    # gated MLP input at batch 1 (llama.rs:301-303): silu(x.Wg^T) * (x.Wu^T),
-    # one launch over both weights, and the two-launch path for comparison
-    from combsengine_amd import _lib as L
-    gpool, gdata = make_pool(QuantFormat.Q4K, 14336, 4096, 0.6 * (1 << 30), seed=1100)
-    upool, _ = make_pool(QuantFormat.Q4K, 14336, 4096, 0.6 * (1 << 30), seed=1101)
-    x = torch.from_numpy(rng.normal(0, 1, (1, 4096)).astype(np.float16)).to(dev)
-    y = torch.empty((1, 14336), dtype=torch.float16, device=dev)
-
-    def gate_up(i):
-        j = i % len(gpool)
-        st = L.lib().cq_matmul_gate_up(gpool[j].handle, upool[j].handle, x.data_ptr(), L.CQ_F16, 1, L.CQ_ACT_SILU,
-                                       y.data_ptr(), L.CQ_F16, torch.cuda.current_stream().cuda_stream)
-        assert st == L.CQ_OK, L.last_error()
-
-    b = 2 * gdata.size + 4096 * 2 + 14336 * 2
-    res = {}
-    for mode in ("1", "0"):
-        os.environ["COMBS_GATEUP_FUSED"] = mode
-        L.reload_options()
-        us, _ = graph_time_us(gate_up, 2 * len(gpool))
-        res["one_launch" if mode == "1" else "two_launches"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1)}
-    os.environ.pop("COMBS_GATEUP_FUSED")
-    L.reload_options()
-    out["gate_up_silu_q4_k_14336x4096_m1"] = res
-    del gpool, upool
-    # decode batch 4 / 16 on the gate shape
-    pool, data = make_pool(QuantFormat.Q4K, 14336, 4096, 0.6 * (1 << 30), seed=1000)
-    for m in (4, 16):
-        x = torch.from_numpy(rng.normal(0, 1, (m, 4096)).astype(np.float16)).to(dev)
-        y = torch.empty((m, 14336), dtype=torch.float32, device=dev)
-        us, _ = graph_time_us(lambda i: pool[i % len(pool)].matmul_into(x, y), 2 * len(pool))
-        b = algo_bytes(data.size, m, 4096, 14336)
-        out[f"q4_k_14336x4096_m{m}"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1)}
-    return out
+        out.append(a.elapsed_time(b) * 1e3 / count)
+    st = stats(out)
+    return st["median"], st
 
 
 def fast_launcher(pool, x, y):
@@ -240,15 +161,243 @@ def fast_launcher(pool, x, y):
     return launch
 
 
-def configs_2_3_5(dev):
-    """BASELINE configs 2, 3 and 5 as eager bursts of launches (HIP events
-    around 2 x pool-size launches on the current stream, best of 3), each
-    launch streaming a distinct weight buffer from a pool larger than the
-    Infinity Cache.  Reported per shape: device us per launch and
-    algorithmic GB/s (weight + x + y bytes)."""
+def load_traffic():
+    p = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(p):
+        with open(p) as f:
+            return json.load(f)
+    return {}
+
+
+def cpu_info():
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "model": model}
+
+
+def _time_calls(fn, seconds):
+    calls, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        calls += 1
+        el = time.perf_counter() - t0
+        if el > seconds:
+            return calls, el
+
+
+def cpu_baseline(seconds=6.0):
+    """The reference CPU path (dequantise once at load, then a dense f32
+    GEMV per call: llama.rs:81-97 -> matmul.rs:34-49, dequant gguf.rs:894-925)
+    restated by the oracle, on a bounded sample of the headline workload (the
+    Q4_K [14336 x 4096] GEMV), 1 thread (the reference's matrixmultiply has
+    no threading) and all cores; the same GB/s metric as the GPU."""
+    import numpy as np
+    import oracle as O
+    from combsengine_amd import QuantFormat
+    n, k = 14336, 4096
+    data = quantized_weight(QuantFormat.Q4K, n, k, 7)
+    t0 = time.perf_counter()
+    w = O.dequant(O.Q4_K, data, n * k, threads=1).reshape(n, k)
+    t_deq = time.perf_counter() - t0
+    x = np.random.default_rng(7).normal(0, 1, (1, k)).astype(np.float16).astype(np.float32)
+    per = algo_bytes(data.size, 1, k, n)
+    c1, e1 = _time_calls(lambda: O.dense_gemm(x, w, 1), seconds / 2)
+    allc = os.cpu_count() or 1
+    cm, em = _time_calls(lambda: O.dense_gemm(x, w, allc), seconds / 2)
+    return {
+        "value": round(per * c1 / e1 / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+        "sample": f"Q4_K [{n}x{k}] m=1 (one of the headline step's two GEMVs): dequantise once "
+                  f"({t_deq:.2f} s, 1 thread), then {c1} dense f32 GEMV calls in {e1:.1f} s on 1 thread "
+                  "(oracle restatement of llama.rs:81-97 -> sgemm)",
+        "all_cores": {"value": round(per * cm / em / 1e9, 3), "cores": allc, "calls": cm},
+        "dequant_s": round(t_deq, 3), "ms_per_call_1t": round(e1 / c1 * 1e3, 3), "cpu": cpu_info(),
+    }
+
+
+def cpu_config1(seconds=4.0):
+    """BASELINE config 1 on the reference CPU path: W [1536 x 576] N(0, 0.02)
+    quantised to Q8_0, x [1 x 576] fp32 N(0, 1); dequantise once (timed
+    separately), then y = x.W^T as a dense f32 GEMV per call, 1 thread and
+    all cores."""
+    import numpy as np
+    import oracle as O
+    from combsengine_amd import QuantFormat, quantize
+    n, k = 1536, 576
+    rng = np.random.default_rng(1)
+    data = np.frombuffer(quantize(QuantFormat.Q8_0, rng.normal(0, 0.02, (n, k)).astype(np.float32)), np.uint8)
+    x = rng.normal(0, 1, (1, k)).astype(np.float32)
+    cd, ed = _time_calls(lambda: O.dequant(O.Q8_0, data, n * k, threads=1), 0.5)
+    w = O.dequant(O.Q8_0, data, n * k, threads=1).reshape(n, k)
+    c1, e1 = _time_calls(lambda: O.dense_gemm(x, w, 1), seconds / 2)
+    allc = os.cpu_count() or 1
+    cm, em = _time_calls(lambda: O.dense_gemm(x, w, allc), seconds / 2)
+    per = algo_bytes(data.size, 1, k, n, xbytes=4)
+    return {"workload": "Q8_0 [1536x576] (SmolLM2-135M MLP gate), x fp32 [1x576], y fp32",
+            "dequant_us": round(ed / cd * 1e6, 2),
+            "gemv_us_1t": round(e1 / c1 * 1e6, 2), "gemv_us_all": round(em / cm * 1e6, 2), "all_cores": allc,
+            "GBps_1t": round(per * c1 / e1 / 1e9, 3), "GBps_all": round(per * cm / em / 1e9, 3),
+            "cpu": cpu_info()}
+
+
+def empty_launch(dev):
+    """Per-launch time of a launch that does no work to speak of (dequantise
+    one 32-value block), back to back in a graph and eagerly."""
+    import torch
+    from combsengine_amd import QuantFormat
+    from combsengine_amd import _lib as L
+    import oracle as O
+    blk = torch.from_numpy(__import__("numpy").frombuffer(O.synth_q8_0(1), "uint8").copy()).to(dev)
+    out = torch.empty(32, device=dev)
+    fn = L.lib().cq_dequantize
+
+    def launch(i):  # (the current stream at call time: the capture stream inside a capture)
+        st = fn(int(QuantFormat.Q8_0), blk.data_ptr(), 34, 32, out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        assert st == L.CQ_OK, L.last_error()
+    g_us, _ = graph_time_us(launch, 200)
+    e_us, _ = eager_time_us(launch, 200)
+    return {"graph_us": round(g_us, 3), "eager_us": round(e_us, 3), "kernel": "cq_dequant_q8_0 (one block)"}
+
+
+def llama3_token(dev, ms=(1, 16)):
+    """Decode tokens/s of one Llama-3-8B token's projection set: 32 layers of
+    q [4096x4096], k and v [1024x4096], o [4096x4096] (Q4_K), the gated
+    gate/up pair [14336x4096] x 2 (one cq_matmul_gate_up call) and down
+    [4096x14336] (Q4_K), then the Q6_K lm_head [128256x4096]; every layer
+    has its own weight buffers (4.3 GB in all), the whole token is one
+    captured graph.  Only the projections are timed (no attention, norms or
+    sampling), so this is the projection-bound decode rate at batch m."""
+    import torch
+    from combsengine_amd import QuantFormat as F
+    from combsengine_amd import QuantWeight
+    from combsengine_amd import _lib as L
+    layers = 32
+    shapes = {"q": (F.Q4K, 4096, 4096), "k": (F.Q4K, 1024, 4096), "v": (F.Q4K, 1024, 4096), "o": (F.Q4K, 4096, 4096),
+              "gate": (F.Q4K, 14336, 4096), "up": (F.Q4K, 14336, 4096), "down": (F.Q4K, 4096, 14336)}
+    bufs, wbytes = {}, 0
+    for i, (name, (fmt, n, k)) in enumerate(shapes.items()):
+        data = quantized_weight(fmt, n, k, 4000 + i)
+        base = torch.from_numpy(data.copy()).to(dev)
+        bufs[name] = [QuantWeight.from_device(fmt, base if l == 0 else base.clone(), n, k) for l in range(layers)]
+        wbytes += layers * data.size
+    hdata = quantized_weight(F.Q6K, 128256, 4096, 4100)
+    head = QuantWeight.from_device(F.Q6K, torch.from_numpy(hdata.copy()).to(dev), 128256, 4096)
+    wbytes += hdata.size
+    out = {"weight_bytes": wbytes, "layers": layers}
+    s = torch.cuda.current_stream().cuda_stream
+    for m in ms:
+        yt = torch.float32 if m == 1 else torch.float16
+        x4 = torch.randn((m, 4096), device=dev).half()
+        x14 = torch.randn((m, 14336), device=dev).half()
+        ys = {n: torch.empty((m, shapes[n][1]), dtype=yt, device=dev) for n in shapes}
+        yh = torch.empty((m, 128256), dtype=yt, device=dev)
+        ydt = L.CQ_F16 if yt == torch.float16 else L.CQ_F32
+
+        def token(_i):
+            for l in range(layers):
+                for name in ("q", "k", "v", "o"):
+                    bufs[name][l].matmul_into(x4, ys[name])
+                st = L.lib().cq_matmul_gate_up(bufs["gate"][l].handle, bufs["up"][l].handle, x4.data_ptr(), L.CQ_F16,
+                                               m, L.CQ_ACT_SILU, ys["gate"].data_ptr(), ydt, s)
+                assert st == L.CQ_OK, L.last_error()
+                bufs["down"][l].matmul_into(x14, ys["down"])
+            head.matmul_into(x4, yh)
+        g = capture(token, 1)
+        st = stats(replay_times(g, 1, 10))
+        us = st["median"]
+        out[f"m{m}"] = {"us_per_token_step": us, "tokens_per_s": round(m * 1e6 / us, 1),
+                        "weight_GBps": round(wbytes / us / 1e3, 1), "launches": layers * 6 + 1, "stats": st}
+    return out
+
+
+def secondary(dev):
+    """Prefill dequant-GEMM (config 4), eager (through fast_launcher: the
+    library may split K) and captured as a graph (no K split under capture)
+    reported separately; lm_head Q6_K; the gated gate/up; batch 4/16."""
     import numpy as np
     import torch
     from combsengine_amd import QuantFormat
+    from combsengine_amd import _lib as L
+    out = {}
+    rng = np.random.default_rng(9)
+    for fmt, n, k in ((QuantFormat.Q4K, 14336, 4096), (QuantFormat.Q6K, 4096, 14336)):
+        pool, data = make_pool(fmt, n, k, 0.3 * (1 << 30), seed=300 + int(fmt))
+        for m in (128, 512, 2048):
+            x = torch.from_numpy(rng.normal(0, 1, (m, k)).astype(np.float16)).to(dev)
+            y = torch.empty((m, n), dtype=torch.float16, device=dev)
+            cnt = 40 if m < 2048 else 16
+            us_e, st_e = eager_time_us(fast_launcher(pool, x, y), cnt, reps=max(3, -(-MIN_LAUNCHES // cnt)))
+            us_g, st_g = graph_time_us(lambda i: pool[i % len(pool)].matmul_into(x, y), cnt,
+                                       reps=max(3, -(-MIN_LAUNCHES // cnt)))
+            fl = 2.0 * m * n * k
+            out[f"prefill_{fmt.name}_{n}x{k}_m{m}"] = {
+                "eager": {"us": us_e, "TFLOPs": round(fl / us_e / 1e6, 1),
+                          "frac_fp16_peak": round(fl / us_e / 1e6 / FP16_PEAK_TFLOPS, 4), "stats": st_e},
+                "graph": {"us": us_g, "TFLOPs": round(fl / us_g / 1e6, 1),
+                          "frac_fp16_peak": round(fl / us_g / 1e6 / FP16_PEAK_TFLOPS, 4), "stats": st_g},
+                "kernels": L.kernels(pool[0], L.CQ_F16, m, L.CQ_F16)}
+        del pool
+    # lm_head Q6_K [128256 x 4096] (431 MB: larger than the Infinity Cache)
+    pool, data = make_pool(QuantFormat.Q6K, 128256, 4096, 2 * 431e6, seed=77)
+    x = torch.from_numpy(rng.normal(0, 1, (1, 4096)).astype(np.float16)).to(dev)
+    y = torch.empty((1, 128256), dtype=torch.float32, device=dev)
+    us, st = graph_time_us(lambda i: pool[i % len(pool)].matmul_into(x, y), 8, reps=13)
+    b = algo_bytes(data.size, 1, 4096, 128256)
+    out["lm_head_q6_k_m1"] = {"us": us, "GBps": round(b / us / 1e3, 1), "stats": st,
+                              "kernel": L.kernels(pool[0], L.CQ_F16, 1, L.CQ_F32)}
+    del pool
+    # gated MLP input at batch 1 (llama.rs:301-303): silu(x.Wg^T) * (x.Wu^T),
+    # one launch over both weights, and the two-launch path for comparison
+    gpool, gdata = make_pool(QuantFormat.Q4K, 14336, 4096, 0.6 * (1 << 30), seed=1100)
+    upool, _ = make_pool(QuantFormat.Q4K, 14336, 4096, 0.6 * (1 << 30), seed=1101)
+    x = torch.from_numpy(rng.normal(0, 1, (1, 4096)).astype(np.float16)).to(dev)
+    y = torch.empty((1, 14336), dtype=torch.float16, device=dev)
+
+    def gate_up(i):
+        j = i % len(gpool)
+        st = L.lib().cq_matmul_gate_up(gpool[j].handle, upool[j].handle, x.data_ptr(), L.CQ_F16, 1, L.CQ_ACT_SILU,
+                                       y.data_ptr(), L.CQ_F16, torch.cuda.current_stream().cuda_stream)
+        assert st == L.CQ_OK, L.last_error()
+
+    b = 2 * gdata.size + 4096 * 2 + 14336 * 2
+    res = {}
+    for mode in ("1", "0"):
+        os.environ["COMBS_GATEUP_FUSED"] = mode
+        L.reload_options()
+        us, st = graph_time_us(gate_up, 2 * len(gpool))
+        res["one_launch" if mode == "1" else "two_launches"] = {"us": us, "GBps": round(b / us / 1e3, 1), "stats": st}
+    os.environ.pop("COMBS_GATEUP_FUSED")
+    L.reload_options()
+    out["gate_up_silu_q4_k_14336x4096_m1"] = res
+    del gpool, upool
+    # decode batch 4 / 16 on the gate shape
+    pool, data = make_pool(QuantFormat.Q4K, 14336, 4096, 0.6 * (1 << 30), seed=1000)
+    for m in (4, 16):
+        x = torch.from_numpy(rng.normal(0, 1, (m, 4096)).astype(np.float16)).to(dev)
+        y = torch.empty((m, 14336), dtype=torch.float32, device=dev)
+        us, st = graph_time_us(lambda i: pool[i % len(pool)].matmul_into(x, y), 2 * len(pool))
+        b = algo_bytes(data.size, m, 4096, 14336)
+        out[f"q4_k_14336x4096_m{m}"] = {"us": us, "GBps": round(b / us / 1e3, 1), "stats": st,
+                                        "kernel": L.kernels(pool[0], L.CQ_F16, m, L.CQ_F32)}
+    return out
+
+
+def configs_2_3_5(dev):
+    """BASELINE configs 2, 3 and 5 as eager bursts of launches (HIP events
+    around bursts of >= 40 launches on the current stream, median over
+    bursts), each launch streaming a distinct weight buffer from a pool
+    larger than the Infinity Cache.  Reported per shape: device us per
+    launch and algorithmic GB/s (weight + x + y bytes)."""
+    import numpy as np
+    import torch
+    from combsengine_amd import QuantFormat
+    from combsengine_amd import _lib as L
     rng = np.random.default_rng(11)
     out = {}
 
@@ -258,9 +407,10 @@ def configs_2_3_5(dev):
         for mm in m:
             x = torch.from_numpy(rng.normal(0, 1, (mm, k)).astype(np.float16)).to(dev)
             y = torch.empty((mm, n), dtype=ydt, device=dev)
-            us = eager_time_us(fast_launcher(pool, x, y), max(2 * len(pool), 40))
+            us, _ = eager_time_us(fast_launcher(pool, x, y), max(2 * len(pool), 40))
             b = algo_bytes(data.size, mm, k, n, ybytes=2 if ydt == torch.float16 else 4)
-            res[f"m{mm}"] = {"us": round(us, 2), "GBps": round(b / us / 1e3, 1)}
+            res[f"m{mm}"] = {"us": us, "GBps": round(b / us / 1e3, 1),
+                             "kernel": L.kernels(pool[0], L.CQ_F16, mm, L.CQ_F16 if ydt == torch.float16 else L.CQ_F32)}
         out[key] = res
         del pool
         return res
@@ -289,8 +439,8 @@ def configs_2_3_5(dev):
         for mm in tot:
             x = torch.from_numpy(rng.normal(0, 1, (mm, k)).astype(np.float16)).to(dev)
             y = torch.empty((mm, n), dtype=torch.float16 if mm > 16 else torch.float32, device=dev)
-            us = eager_time_us(fast_launcher(pool, x, y), max(2 * len(pool), 40))
-            per[f"m{mm}"] = round(us, 2)
+            us, _ = eager_time_us(fast_launcher(pool, x, y), max(2 * len(pool), 40))
+            per[f"m{mm}"] = us
             tot[mm] += us
         sweep[name] = per
         del pool
@@ -321,6 +471,7 @@ def main():
     import numpy as np
     import torch
     from combsengine_amd import QuantFormat
+    from combsengine_amd import _lib as L
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -344,53 +495,74 @@ def main():
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-    # the K timed steps, captured once and replayed (timing brackets the replay)
+    # The K timed steps, captured once (starting on buffers the warmup did not
+    # touch) and replayed; the first replay is the timed region.
+    K, W = args.steps, args.warmup
     t_cap = time.perf_counter()
-    us_per_step, graph = graph_time_us(step, args.steps, reps=1)
+    g = capture(lambda i: step(W + i), K)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    ms_total = a.elapsed_time(b)
     wall = time.perf_counter() - t_cap
-    ms_total = us_per_step * args.steps / 1e3
     step_bytes = sum(algo_bytes(sz, 1, k, n) for sz, (n, k) in zip(sizes, shapes))
-    value = step_bytes * args.steps / (ms_total / 1e3) / 1e9
+    value = step_bytes * K / (ms_total / 1e3) / 1e9
+    # more replays of the same graph until >= MIN_LAUNCHES launches are timed
+    reps = max(5, -(-MIN_LAUNCHES // (len(shapes) * K)))
+    step_stats = stats([t for t in replay_times(g, K, reps)])
+    del g
 
-    # Dominant kernel: launches of one shape back to back in a graph.
+    # Dominant kernel: >= MIN_LAUNCHES launches of one shape back to back in a graph.
     launch, tot_b, tot_us = {}, 0.0, 0.0
     traffic = load_traffic().get(HEADLINE_KERNEL, {})
     for s, (n, k) in enumerate(shapes):
-        us, _ = graph_time_us(lambda i, s=s: pools[s][i % P].matmul_into(xs[s], ys[s]), 4 * P)
-        b = algo_bytes(sizes[s], 1, k, n)
-        launch[f"{n}x{k}"] = {"us": round(us, 3), "GBps": round(b / us / 1e3, 1),
-                              "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
-        tot_b += b
+        us, st = graph_time_us(lambda i, s=s: pools[s][i % P].matmul_into(xs[s], ys[s]), max(MIN_LAUNCHES, 4 * P))
+        bb = algo_bytes(sizes[s], 1, k, n)
+        launch[f"{n}x{k}"] = {"us": us, "GBps": round(bb / us / 1e3, 1), "frac": round(bb / us / 1e3 / HBM_PEAK_GBS, 4),
+                              "stats": st, "kernel": L.kernels(pools[s][0], L.CQ_F16, 1, L.CQ_F32)}
+        tot_b += bb
         tot_us += us
     achieved = tot_b / tot_us / 1e3
     t_bytes = [traffic.get(f"{n}x{k}") for (n, k) in shapes]
     traffic_val = round(sum(t_bytes) / len(t_bytes)) if all(t_bytes) else None
+    del pools
 
-    extra = {} if args.no_extra else secondary(dev)
+    extra = {"empty_launch": empty_launch(dev)}
+    if not args.no_extra:
+        extra["llama3_8b_decode_token"] = llama3_token(dev)
+        extra.update(secondary(dev))
     if not args.no_extra and not args.no_configs:
         extra["configs"] = configs_2_3_5(dev)
     prefill = {k: v for k, v in extra.items() if k.startswith("prefill_")}
-    best_prefill = max((v["TFLOPs"] for v in prefill.values()), default=None)
+    best_prefill = max((v["eager"]["TFLOPs"] for v in prefill.values()), default=None)
+    tok = extra.get("llama3_8b_decode_token", {}).get("m1", {})
 
     line = {
         "metric": "Q4_K decode GEMV HBM GB/s (% of peak); prefill dequant-GEMM TFLOP/s",
-        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(ms_total / args.steps, 5), "higher_is_better": True, "scaling": "weak",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(ms_total / K, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "q4_k", "data": "synthetic",
         "config": {"workload": "Q4_K decode GEMV, Llama-3-8B shapes [14336x4096]+[4096x14336], batch 1, x f16, "
                                f"y f32; weight pool {P} x {len(shapes)} buffers ({P * sum(sizes) / 2**30:.2f} GiB)",
                    "global_batch": 1, "parallelism": "none (1 GPU)"},
         "frac_of_hbm_peak": round(value / HBM_PEAK_GBS, 4),
+        "step_us": step_stats,
         "roofline": {"bound": "hbm", "kernel": HEADLINE_KERNEL, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": traffic_val,
                      "algorithmic_bytes_per_launch": round(tot_b / len(shapes)), "launches": launch},
+        "empty_launch_us": extra["empty_launch"],
+        "tokens_per_s": tok.get("tokens_per_s"),
         "prefill_TFLOPs_best": best_prefill,
         "wall_s_capture_and_replay": round(wall, 3),
         "secondary": extra,
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
+        line["cpu_config1"] = cpu_config1()
     print(json.dumps(line), flush=True)
 
 

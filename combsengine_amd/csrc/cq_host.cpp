@@ -683,18 +683,19 @@ static cq_status launch_gemv1k(DeviceModule* dm, const cq_weight* w, const void*
 // ceil(4 units / 64) waves, 8 / C row groups per workgroup of up to 8
 // waves, one workgroup per compute unit, each wave with four rows of loads
 // in flight; the activation row is staged by every thread in 1, 2, 4 or 8
-// 16-byte pieces.  The default for Q4_K rows whose quarters do not fill a
-// whole number of waves (units % 16 != 0), where cq_gemv1 leaves lanes
-// idle: Qwen2.5-7B 3584 x 3584 5.75 against 6.05 us, 18944 x 3584 11.9
+// 16-byte pieces.  Measured against cq_gemv1 on Q4_K rows whose quarters do
+// not fill whole waves, where cq_gemv1 leaves lanes idle: Qwen2.5-7B 3584 x 3584 5.75 against 6.05 us, 18944 x 3584 11.9
 // against 13.7, 3584 x 18944 13.9 against 14.5 (cq_gemv1k); on the
 // Llama-3-8B shapes (16 and 56 units) cq_gemv1 measured faster (9.7 against
-// 10.2 us at 14336 x 4096).  COMBS_GEMVR=0 never, 2 always where it fits.
+// 10.2 us at 14336 x 4096, 10.4 against 10.6 at 4096 x 14336).  So it is the
+// default below 16 units and above 64 (where cq_gemv1k would run).
+// COMBS_GEMVR=0 never, 2 always where it fits.
 constexpr int kGvrMaxK = 32768;
 constexpr int kGvrWaves = 8;
 static bool gemvr_fits(const cq_weight* w) {
   return w->format == CQ_Q4_K && w->k % 256 == 0 && w->k <= kGvrMaxK;
 }
-static bool gemvr_default(const cq_weight* w) { return (w->k / 256) % 16 != 0; }
+static bool gemvr_default(const cq_weight* w) { return w->k / 256 < 16 || w->k / 256 > 64; }
 static cq_status launch_gemvr(DeviceModule* dm, const cq_weight* w, const void* x, void* y, int yt, hipStream_t s,
                               const CqEpi& epi) {
   GvrArgs a{};

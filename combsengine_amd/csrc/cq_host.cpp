@@ -176,6 +176,16 @@ struct GvrArgs {
   int N, K, units, C, G, iters;
   CqEpi epi;
 };
+struct GvsArgs {
+  const void* w;
+  const void* x;
+  void* y;
+  float* part;
+  long long row_bytes;
+  long long wbytes;
+  int M, N, K, units, usplit;
+  CqEpi epi;
+};
 struct DequantArgs {
   const void* w;
   float* out;
@@ -201,6 +211,7 @@ struct DeviceModule {
   hipFunction_t gemv1k[kNumFormats][2][2] = {};   // rows of 65-128 units, Q4_K / Q5_K / Q6_K / Q4_0 [format][y f16][epilogue]
   hipFunction_t gemv2[kNumFormats][2][2] = {};  // K-quants only     // [format][y f16]
   hipFunction_t gemvd[kNumFormats][3][2] = {};  // K-quants only: [format][NT 1, 2, 4][y f16]
+  hipFunction_t gemvs[kNumFormats][2] = {};  // K-quants only: [format][y f16]
   hipFunction_t gemvr[2][4] = {};  // Q4_K rows split across lanes: [y f16][log2 activation pieces per thread]
   int cus = 0;                        // compute units of the device
 };
@@ -316,6 +327,16 @@ void load_module(DeviceModule& d, int dev) {
         }
       }
   }
+  for (int fi = 0; fi < kNumFormats; fi++) {
+    if (block_values(kFormats[fi]) != 256) continue;
+    for (int yt = 0; yt < 2; yt++) {
+      snprintf(name, sizeof name, "cq_gemvs_%s_y%s", fmt_name(kFormats[fi]), yt ? "f16" : "f32");
+      if (get(&d.gemvs[fi][yt], name) != hipSuccess) {
+        d.err = std::string("missing kernel ") + name;
+        return;
+      }
+    }
+  }
   for (int yt = 0; yt < 2; yt++)
     for (int xl = 0; xl < 4; xl++) {
       snprintf(name, sizeof name, "cq_gemvr_q4_k_y%s_x%d", yt ? "f16" : "f32", 1 << xl);
@@ -356,7 +377,7 @@ constexpr int kUnset = -1000000;
 struct Knobs {
   int gemv_waves, gemv1, gemv1k, gemv1_grid, gemv1_i8, gemv1_prefetch2, gemv1_span, gemv1_spread,
       gemv1_wave_major, gemv2, gemv2_wpc, gemvd, gvd_nt, gvd_waves, gemm_kernel, gemm_waves, gemm2_mt,
-      gemm2_nt, gemm2_split, gateup_fused, gemvr;
+      gemm2_nt, gemm2_split, gateup_fused, gemvr, gemvs, gemvs_split;
 };
 Knobs g_knobs;
 std::once_flag g_knobs_once;
@@ -388,6 +409,8 @@ void read_knobs() {
   k.gemm2_split = env_int("COMBS_GEMM2_SPLIT", 0);
   k.gateup_fused = env_int("COMBS_GATEUP_FUSED", 1);
   k.gemvr = env_int("COMBS_GEMVR", 1);
+  k.gemvs = env_int("COMBS_GEMVS", 1);
+  k.gemvs_split = env_int("COMBS_GEMVS_SPLIT", 0);
   g_knobs = k;
 }
 const Knobs& knobs() {
@@ -608,6 +631,79 @@ static cq_status launch_gemvd(DeviceModule* dm, const cq_weight* w, const void* 
   void* params[] = {&a};
   HIP_TRY(klaunch(dm, dm->gemvd[fi][nt == 1 ? 0 : nt == 2 ? 1 : 2][yt], (unsigned)wgs, 1, 1, 64 * nw, 0, s,
                   params));
+  return CQ_OK;
+}
+
+// Batched decode with the activations shared through LDS (cq_gemvs_*,
+// K-quants, 2 <= m <= 16): workgroups of 8 waves x 16 rows; optionally the
+// superblocks split over blockIdx.y (slices of >= 2 superblocks, the
+// slices' fp32 partials summed by cq_splitk_reduce_* in slice order).
+// Needs the weight 16-byte aligned and a multiple of 16 bytes (its LDS DMA
+// reads whole 16-byte pieces).  Measured against cq_gemvd_* (eager bursts):
+// it wins where 128-row groups alone fill the compute units -- Q6_K lm_head
+// 128256 x 4096 at m = 2 / 4 / 8 / 16: 138 / 140 / 143 / 143 us against
+// 146 / 147 / 154 / 171 -- and loses on smaller weights, where it needs the
+// split (its per-call scratch allocation and reduction launch cost more
+// than they save: Q4_K 14336 x 4096 at m = 4 21.9 against 14.8 us).  So by
+// default it serves weights of at least one 128-row group per compute unit,
+// unsplit (no scratch, so also under graph capture); COMBS_GEMVS=2 uses it
+// for every K-quant weight it fits (splitting automatically, not under
+// capture), COMBS_GEMVS_SPLIT forces the slice count, COMBS_GEMVS=0 never.
+constexpr int kGvsWaves = 8;
+static bool gemvs_fits(const cq_weight* w) {
+  return block_values(w->format) == 256 && (reinterpret_cast<uintptr_t>(w->dev) & 15) == 0 && w->nbytes % 16 == 0;
+}
+static cq_status launch_gemvs(DeviceModule* dm, const cq_weight* w, const void* x, int64_t m, void* y, int yt,
+                              hipStream_t s, const CqEpi& epi) {
+  const int fi = fmt_index(w->format);
+  GvsArgs a{};
+  a.w = w->dev;
+  a.x = x;
+  a.y = y;
+  a.part = nullptr;
+  a.row_bytes = (long long)(w->nbytes / (size_t)w->n);
+  a.wbytes = (long long)w->nbytes;
+  a.M = (int)m;
+  a.N = (int)w->n;
+  a.K = (int)w->k;
+  a.units = (int)(w->k / 256);
+  a.epi = epi;
+  const long long groups = (w->n + 16 * kGvsWaves - 1) / (16 * kGvsWaves);
+  if (groups > 0x7fffffffLL) return fail(CQ_ERR_BAD_SHAPE, "grid too large (n=%lld)", (long long)w->n);
+  int splits = knobs().gemvs_split;
+  if (splits < 1) {
+    splits = knobs().gemvs == 2 ? (int)((dm->cus + groups - 1) / groups) : 1;
+    if (splits > a.units / 2) splits = a.units / 2;
+    if (splits < 1) splits = 1;
+  }
+  if (splits > a.units) splits = a.units;
+  auto part_size = [&](int sp) -> size_t {
+    const int us = (a.units + sp - 1) / sp;
+    const int n_sp = (a.units + us - 1) / us;
+    return n_sp > 1 ? (size_t)n_sp * m * w->n * 4 : 0;
+  };
+  if (g_fixed)
+    while (splits > 1 && part_size(splits) > g_fixed->bytes) splits /= 2;
+  a.usplit = (a.units + splits - 1) / splits;
+  splits = (a.units + a.usplit - 1) / a.usplit;
+  const size_t part_bytes = part_size(splits);
+  void* ws = nullptr;
+  if (part_bytes) {
+    if (g_fixed) ws = g_fixed->ptr;
+    else if (!g_plan) HIP_TRY(hipMallocAsync(&ws, part_bytes, s));
+    a.part = (float*)ws;
+  }
+  void* params[] = {&a};
+  hipError_t e = klaunch(dm, dm->gemvs[fi][yt], (unsigned)groups, (unsigned)splits, 1, 64 * kGvsWaves, 0, s, params);
+  if (e == hipSuccess && part_bytes) {
+    long long mn = m * w->n;
+    int n = (int)w->n;
+    CqEpi ep = epi;
+    void* rp[] = {&a.part, &y, &splits, &mn, &n, &ep};
+    e = klaunch(dm, dm->reduce[yt], (unsigned)((mn + 255) / 256), 1, 1, 256, 0, s, rp);
+  }
+  if (ws && !g_fixed) HIP_TRY(hipFreeAsync(ws, s));
+  if (e != hipSuccess) return fail(CQ_ERR_HIP, "batched decode launch: %s", hipGetErrorString(e));
   return CQ_OK;
 }
 
@@ -979,6 +1075,15 @@ static cq_status matmul_impl(const cq_weight* w, const void* x, int x_dtype, int
     if (gemv1_fits(w)) return launch_gemv1(dm, w, x, y, yt, (hipStream_t)stream, epi);
     if (gemv1k_fits(w) && knobs().gemv1k) return launch_gemv1k(dm, w, x, y, yt, (hipStream_t)stream, epi);
     if (kq && w->k / 256 <= 64 && gemv2_fits(w)) return launch_gemv2(dm, w, x, y, yt, (hipStream_t)stream, epi);
+  }
+  if (kq && !xt && m >= 2 && m <= 16 && gemvs_fits(w)) {
+    if (knobs().gemvs == 1 && w->n >= (int64_t)16 * kGvsWaves * dm->cus)
+      return launch_gemvs(dm, w, x, m, y, yt, (hipStream_t)stream, epi);  // unsplit: no scratch
+    if (knobs().gemvs == 2 || knobs().gemvs_split >= 1) {
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      if (!g_plan) HIP_TRY(hipStreamIsCapturing((hipStream_t)stream, &cs));
+      if (cs == hipStreamCaptureStatusNone) return launch_gemvs(dm, w, x, m, y, yt, (hipStream_t)stream, epi);
+    }
   }
   if (kq && !xt && m >= 2 && m <= 16 && knobs().gemvd)
     return launch_gemvd(dm, w, x, m, y, yt, (hipStream_t)stream, epi);

@@ -6,6 +6,7 @@
 // kernels (cq_dequant_*).
 #include "cq_gemv.h"
 #include "cq_gemvd.h"
+#include "cq_gemvs.h"
 #include "cq_dequant.h"
 
 #define GEMV_KERNEL(NAME, FMT, XT, YT)                                               \
@@ -61,3 +62,14 @@ GEMVD_FMT(q4_k, CQ_Q4_K)
 GEMVD_FMT(q5_k, CQ_Q5_K)
 GEMVD_FMT(q6_k, CQ_Q6_K)
 
+
+// Batched decode with the activations shared through LDS and the K range
+// split over workgroups (cq_gemvs.h).
+#define GEMVS_KERNEL(NAME, FMT, YT) \
+  extern "C" __global__ void __launch_bounds__(64 * GVS_WAVES) NAME(const GvsArgs a) { gemvs_body<FMT, YT>(a); }
+GEMVS_KERNEL(cq_gemvs_q4_k_yf32, CQ_Q4_K, 0)
+GEMVS_KERNEL(cq_gemvs_q4_k_yf16, CQ_Q4_K, 1)
+GEMVS_KERNEL(cq_gemvs_q5_k_yf32, CQ_Q5_K, 0)
+GEMVS_KERNEL(cq_gemvs_q5_k_yf16, CQ_Q5_K, 1)
+GEMVS_KERNEL(cq_gemvs_q6_k_yf32, CQ_Q6_K, 0)
+GEMVS_KERNEL(cq_gemvs_q6_k_yf16, CQ_Q6_K, 1)

@@ -313,6 +313,7 @@ def test_graph_capture_replays(cuda, monkeypatch):
     decode of a 74-superblock Q6_K row (the row-half kernel)."""
     import torch
     monkeypatch.setenv("COMBS_GEMM2_SPLIT", "1")
+    monkeypatch.setenv("COMBS_GEMVS", "0")  # captured batched decode runs cq_gemvd_*: the eager reference too
     fmt, n, k = QuantFormat.Q4K, 512, 4096
     rng = np.random.default_rng(3)
     data = quantize(fmt, rng.normal(0, 0.02, (n, k)).astype(np.float32))
@@ -356,11 +357,12 @@ def test_graph_capture_replays(cuda, monkeypatch):
                                    (500, 1792, 9)])
 def test_gemv_batched_direct(cuda, monkeypatch, fmt, nt, nw, n, k, m):
     """Batched decode (2 <= m <= 16, fp16 x) through the direct-activation
-    kernel: NT row tiles per workgroup (ragged last tile), waves splitting
+    kernel (cq_gemvd_*): NT row tiles per workgroup (ragged last tile), waves splitting
     the superblocks (more waves than superblocks, uneven shares, tails
     shorter than the load pipeline), m not a multiple of 4; checked against
     the oracle and bit-for-bit stable over repeated launches."""
     import torch
+    monkeypatch.setenv("COMBS_GEMVS", "0")  # cq_gemvd_*, not the LDS-shared kernel
     monkeypatch.setenv("COMBS_GVD_NT", nt)
     monkeypatch.setenv("COMBS_GVD_WAVES", nw)
     data = synth(fmt, n, k)
@@ -393,14 +395,14 @@ def test_gemv_batched_gaussian_llama_shape(cuda, fmt, m):
     O.assert_close(got, O.ref_matmul(x, wd), 1e-3, "oracle")
     f64 = (torch.from_numpy(x).double() @ torch.from_numpy(wd).double().T).numpy()
     O.assert_close(got, f64, 1e-3, "f64")
-    os.environ["COMBS_GEMVD"] = "0"
-    L.reload_options()
-    try:
-        old = _run(w, x, torch.float16, torch.float32)
-    finally:
-        os.environ.pop("COMBS_GEMVD")
+    for knob in ("COMBS_GEMVS", "COMBS_GEMVD"):  # the direct-activation kernel, then the 16-row MFMA GEMV
+        os.environ[knob] = "0"
         L.reload_options()
-    O.assert_close(got, old, 1e-3, "mfma gemv")
+        old = _run(w, x, torch.float16, torch.float32)
+        O.assert_close(got, old, 1e-3, f"with {knob}=0")
+    os.environ.pop("COMBS_GEMVS")
+    os.environ.pop("COMBS_GEMVD")
+    L.reload_options()
 
 
 @pytest.mark.parametrize("fmt", [QuantFormat.Q4K, QuantFormat.Q5K, QuantFormat.Q6K, QuantFormat.Q4_0, QuantFormat.Q8_0])
@@ -432,3 +434,38 @@ def test_gemv_single_row_long_k(cuda, monkeypatch, fmt, n, k, kernel):
     O.assert_close(a, expect, rel_of(fmt), "y32")
     assert np.array_equal(a.view(np.uint32), _run(w, x, torch.float16, torch.float32).view(np.uint32))
     O.assert_close(_run(w, x, torch.float16, torch.float16), expect, 1e-3, "y16")
+
+
+@pytest.mark.parametrize("fmt", KQ)
+@pytest.mark.parametrize("split", ["0", "1", "3"])
+@pytest.mark.parametrize("n,k,m", [(300, 4096, 2), (35, 512, 16), (97, 3584, 7), (70, 14336, 4), (33, 256, 16),
+                                   (500, 1792, 9), (1000, 2048, 16), (129, 4608, 3)])
+def test_gemv_batched_shared(cuda, monkeypatch, fmt, split, n, k, m):
+    """Batched decode (2 <= m <= 16, fp16 x) through the LDS-shared kernel
+    (cq_gemvs_*): 128-row workgroups (ragged last group and tile), slices of
+    the superblocks over the grid (automatic, one, three: ragged last slice,
+    slices shorter than the 4-slot ring), fp32 and fp16 y, the bias epilogue
+    on both the direct and the split path; against the oracle and bit-for-bit
+    stable over repeated launches."""
+    import torch
+    monkeypatch.setenv("COMBS_GEMVS", "2")
+    monkeypatch.setenv("COMBS_GEMVS_SPLIT", split)
+    data = synth(fmt, n, k)
+    wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
+    w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
+    x = O.x_pattern(m, k, 13, 31, 15.0, 16.0).reshape(m, k)
+    expect = O.ref_matmul(x, wd)
+    xd = torch.from_numpy(x).cuda().half()
+    kern = L.path_name(w, xd, torch.empty((m, n), device="cuda"))
+    print(f"gemvs {fmt.name} split={split} n={n} k={k} m={m} kernels={kern}", flush=True)
+    # (the LDS DMA reads whole 16-byte pieces: a weight whose size is not a
+    # multiple of 16 bytes takes cq_gemvd_*)
+    assert kern.startswith("cq_gemvs_" if len(data) % 16 == 0 else "cq_gemvd_")
+    a = _run(w, x, torch.float16, torch.float32)
+    O.assert_close(a, expect, 1e-3, "y32")
+    O.assert_close(_run(w, x, torch.float16, torch.float16), expect, 1e-3, "y16")
+    assert np.array_equal(a.view(np.uint32), _run(w, x, torch.float16, torch.float32).view(np.uint32))
+    b = np.linspace(-1, 1, n).astype(np.float32)
+    yb = torch.empty((m, n), device="cuda")
+    w.matmul_bias_into(xd, torch.from_numpy(b).cuda(), yb)
+    O.assert_close(yb.cpu().numpy(), expect.astype(np.float64) + b, 1e-3, "bias")

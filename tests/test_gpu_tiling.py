@@ -123,6 +123,7 @@ def test_gemvd_row_tiles_bit_identical(cuda, monkeypatch, fmt, nw):
     n, k, m = 600, 4096, 9
     data, w = _weight(fmt, n, k, 950 + int(fmt))
     x = torch.from_numpy(_x(m, k, 10)).cuda().half()
+    monkeypatch.setenv("COMBS_GEMVS", "0")  # cq_gemvd_*
     monkeypatch.setenv("COMBS_GVD_WAVES", nw)
     outs = {}
     for nt in ("1", "2", "4"):

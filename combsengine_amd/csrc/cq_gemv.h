@@ -301,16 +301,24 @@ __device__ __forceinline__ void load_q40(FragQ40& f, const uint8_t* b, int g, in
     f.d[i] = ld_u16(b + 18 * ii);
   }
 }
-template <int XT>
-__device__ __forceinline__ void compute_q40(const FragQ40& f, const XRow<XT>& xr, int k0, int g, int nb, f4& acc) {
+// B operand of block i (values k = 4g..4g+3 from the low nibbles of qs
+// bytes 4g..4g+3, then k = 16+4g..16+4g+3 from their high nibbles: the A
+// side reads x at the same k, load_a4x2) and the block's fp16 scale.
+__device__ __forceinline__ h8 legacy_b(const FragQ40& f, int i, int g) {
+  (void)g;
   const h2 one = hsplat(1.0f), c_lo = hsplat(-1032.0f);
   const h2 s16 = hsplat(0.0625f), c_hi = hsplat(-72.0f);
+  const uint32_t p1 = perm(C64, f.q[i], SEL_B0_E_B1_E), p2 = perm(C64, f.q[i], SEL_B2_E_B3_E);
+  return mk_h8(pk_fma(p1 & 0x640F640Fu, one, c_lo), pk_fma(p2 & 0x640F640Fu, one, c_lo),
+               pk_fma(p1 & 0x64F064F0u, s16, c_hi), pk_fma(p2 & 0x64F064F0u, s16, c_hi));
+}
+__device__ __forceinline__ uint32_t legacy_d(const FragQ40& f, int i) { return f.d[i]; }
+template <int XT>
+__device__ __forceinline__ void compute_q40(const FragQ40& f, const XRow<XT>& xr, int k0, int g, int nb, f4& acc) {
 #pragma unroll
   for (int i = 0; i < LB; i++) {
     if (i >= nb) break;
-    const uint32_t p1 = perm(C64, f.q[i], SEL_B0_E_B1_E), p2 = perm(C64, f.q[i], SEL_B2_E_B3_E);
-    const h8 b = mk_h8(pk_fma(p1 & 0x640F640Fu, one, c_lo), pk_fma(p2 & 0x640F640Fu, one, c_lo),
-                       pk_fma(p1 & 0x64F064F0u, s16, c_hi), pk_fma(p2 & 0x64F064F0u, s16, c_hi));
+    const h8 b = legacy_b(f, i, g);
     const int kb = k0 + 32 * i;
     const A8<XT> a = load_a4x2<XT>(xr, kb + 4 * g, kb + 16 + 4 * g);
     const f4 c = mfma_x<XT>(a, b, f4{0, 0, 0, 0});
@@ -339,22 +347,26 @@ __device__ __forceinline__ void load_q50(FragQ50& f, const uint8_t* b, int g, in
 __device__ __forceinline__ uint32_t spread4(uint32_t v) {
   return ((v & 0xFu) * 0x00204081u) & 0x01010101u;
 }
-template <int XT>
-__device__ __forceinline__ void compute_q50(const FragQ50& f, const XRow<XT>& xr, int k0, int g, int nb, f4& acc) {
+__device__ __forceinline__ h8 legacy_b(const FragQ50& f, int i, int g) {
   const h2 one = hsplat(1.0f), c_lo = hsplat(-1040.0f);
   const h2 s16 = hsplat(0.0625f), c_hi = hsplat(-80.0f);
+  const uint32_t q = f.q[i];
+  const uint32_t hl = spread4(f.h[i] >> (4 * g));
+  const uint32_t hh = spread4(f.h[i] >> (16 + 4 * g));
+  const uint32_t z = bfi(0x10101010u, hl << 4, q);
+  const uint32_t hx = hh | C64;
+  return mk_h8(pk_fma(perm(C64, z, SEL_B0_E_B1_E) & 0x641F641Fu, one, c_lo),
+               pk_fma(perm(C64, z, SEL_B2_E_B3_E) & 0x641F641Fu, one, c_lo),
+               pk_fma(perm(hx, q, SEL_X_B01) & 0x65F065F0u, s16, c_hi),
+               pk_fma(perm(hx, q, SEL_X_B23) & 0x65F065F0u, s16, c_hi));
+}
+__device__ __forceinline__ uint32_t legacy_d(const FragQ50& f, int i) { return f.d[i]; }
+template <int XT>
+__device__ __forceinline__ void compute_q50(const FragQ50& f, const XRow<XT>& xr, int k0, int g, int nb, f4& acc) {
 #pragma unroll
   for (int i = 0; i < LB; i++) {
     if (i >= nb) break;
-    const uint32_t q = f.q[i];
-    const uint32_t hl = spread4(f.h[i] >> (4 * g));
-    const uint32_t hh = spread4(f.h[i] >> (16 + 4 * g));
-    const uint32_t z = bfi(0x10101010u, hl << 4, q);
-    const uint32_t hx = hh | C64;
-    const h8 b = mk_h8(pk_fma(perm(C64, z, SEL_B0_E_B1_E) & 0x641F641Fu, one, c_lo),
-                       pk_fma(perm(C64, z, SEL_B2_E_B3_E) & 0x641F641Fu, one, c_lo),
-                       pk_fma(perm(hx, q, SEL_X_B01) & 0x65F065F0u, s16, c_hi),
-                       pk_fma(perm(hx, q, SEL_X_B23) & 0x65F065F0u, s16, c_hi));
+    const h8 b = legacy_b(f, i, g);
     const int kb = k0 + 32 * i;
     const A8<XT> a = load_a4x2<XT>(xr, kb + 4 * g, kb + 16 + 4 * g);
     const f4 c = mfma_x<XT>(a, b, f4{0, 0, 0, 0});
@@ -404,38 +416,46 @@ __device__ __forceinline__ void affine_block(const A8<XT>& a, const h8& b, uint3
 #pragma unroll
   for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(d, c[r], __builtin_fmaf(m, s[r], acc[r]));
 }
-template <int XT>
-__device__ __forceinline__ void compute_q41(const FragQ41& f, const XRow<XT>& xr, int k0, int g, int nb, f4& acc) {
+// B = q (no offset) for the affine formats; d and m in one word.
+__device__ __forceinline__ h8 legacy_b(const FragQ41& f, int i, int g) {
+  (void)g;
   const h2 one = hsplat(1.0f), c_lo = hsplat(-1024.0f);
   const h2 s16 = hsplat(0.0625f), c_hi = hsplat(-64.0f);
+  const uint32_t p1 = perm(C64, f.q[i], SEL_B0_E_B1_E), p2 = perm(C64, f.q[i], SEL_B2_E_B3_E);
+  return mk_h8(pk_fma(p1 & 0x640F640Fu, one, c_lo), pk_fma(p2 & 0x640F640Fu, one, c_lo),
+               pk_fma(p1 & 0x64F064F0u, s16, c_hi), pk_fma(p2 & 0x64F064F0u, s16, c_hi));
+}
+__device__ __forceinline__ uint32_t legacy_d(const FragQ41& f, int i) { return f.dm[i]; }
+__device__ __forceinline__ h8 legacy_b(const FragQ51& f, int i, int g) {
+  const h2 one = hsplat(1.0f), c_lo = hsplat(-1024.0f);
+  const h2 s16 = hsplat(0.0625f), c_hi = hsplat(-64.0f);
+  const uint32_t q = f.q[i];
+  const uint32_t hl = spread4(f.h[i] >> (4 * g));
+  const uint32_t hh = spread4(f.h[i] >> (16 + 4 * g));
+  const uint32_t z = bfi(0x10101010u, hl << 4, q);
+  const uint32_t hx = hh | C64;
+  return mk_h8(pk_fma(perm(C64, z, SEL_B0_E_B1_E) & 0x641F641Fu, one, c_lo),
+               pk_fma(perm(C64, z, SEL_B2_E_B3_E) & 0x641F641Fu, one, c_lo),
+               pk_fma(perm(hx, q, SEL_X_B01) & 0x65F065F0u, s16, c_hi),
+               pk_fma(perm(hx, q, SEL_X_B23) & 0x65F065F0u, s16, c_hi));
+}
+__device__ __forceinline__ uint32_t legacy_d(const FragQ51& f, int i) { return f.dm[i]; }
+template <int XT>
+__device__ __forceinline__ void compute_q41(const FragQ41& f, const XRow<XT>& xr, int k0, int g, int nb, f4& acc) {
 #pragma unroll
   for (int i = 0; i < LB; i++) {
     if (i >= nb) break;
-    const uint32_t p1 = perm(C64, f.q[i], SEL_B0_E_B1_E), p2 = perm(C64, f.q[i], SEL_B2_E_B3_E);
-    const h8 b = mk_h8(pk_fma(p1 & 0x640F640Fu, one, c_lo), pk_fma(p2 & 0x640F640Fu, one, c_lo),
-                       pk_fma(p1 & 0x64F064F0u, s16, c_hi), pk_fma(p2 & 0x64F064F0u, s16, c_hi));
     const int kb = k0 + 32 * i;
-    affine_block<XT>(load_a4x2<XT>(xr, kb + 4 * g, kb + 16 + 4 * g), b, f.dm[i], acc);
+    affine_block<XT>(load_a4x2<XT>(xr, kb + 4 * g, kb + 16 + 4 * g), legacy_b(f, i, g), f.dm[i], acc);
   }
 }
 template <int XT>
 __device__ __forceinline__ void compute_q51(const FragQ51& f, const XRow<XT>& xr, int k0, int g, int nb, f4& acc) {
-  const h2 one = hsplat(1.0f), c_lo = hsplat(-1024.0f);
-  const h2 s16 = hsplat(0.0625f), c_hi = hsplat(-64.0f);
 #pragma unroll
   for (int i = 0; i < LB; i++) {
     if (i >= nb) break;
-    const uint32_t q = f.q[i];
-    const uint32_t hl = spread4(f.h[i] >> (4 * g));
-    const uint32_t hh = spread4(f.h[i] >> (16 + 4 * g));
-    const uint32_t z = bfi(0x10101010u, hl << 4, q);
-    const uint32_t hx = hh | C64;
-    const h8 b = mk_h8(pk_fma(perm(C64, z, SEL_B0_E_B1_E) & 0x641F641Fu, one, c_lo),
-                       pk_fma(perm(C64, z, SEL_B2_E_B3_E) & 0x641F641Fu, one, c_lo),
-                       pk_fma(perm(hx, q, SEL_X_B01) & 0x65F065F0u, s16, c_hi),
-                       pk_fma(perm(hx, q, SEL_X_B23) & 0x65F065F0u, s16, c_hi));
     const int kb = k0 + 32 * i;
-    affine_block<XT>(load_a4x2<XT>(xr, kb + 4 * g, kb + 16 + 4 * g), b, f.dm[i], acc);
+    affine_block<XT>(load_a4x2<XT>(xr, kb + 4 * g, kb + 16 + 4 * g), legacy_b(f, i, g), f.dm[i], acc);
   }
 }
 
@@ -454,17 +474,20 @@ __device__ __forceinline__ void load_q80(FragQ80& f, const uint8_t* b, int g, in
     f.q[i] = ld_u64(b + 34 * ii + 2 + 8 * g);
   }
 }
+__device__ __forceinline__ h8 legacy_b(const FragQ80& f, int i, int g) {
+  (void)g;
+  const h2 one = hsplat(1.0f), cb = hsplat(-1152.0f);
+  const uint32_t x0 = f.q[i].x ^ 0x80808080u, x1 = f.q[i].y ^ 0x80808080u;
+  return mk_h8(pk_fma(perm(0x64646464u, x0, 0x04010400u), one, cb), pk_fma(perm(0x64646464u, x0, 0x04030402u), one, cb),
+               pk_fma(perm(0x64646464u, x1, 0x04010400u), one, cb), pk_fma(perm(0x64646464u, x1, 0x04030402u), one, cb));
+}
+__device__ __forceinline__ uint32_t legacy_d(const FragQ80& f, int i) { return f.d[i]; }
 template <int XT>
 __device__ __forceinline__ void compute_q80(const FragQ80& f, const XRow<XT>& xr, int k0, int g, int nb, f4& acc) {
-  const h2 one = hsplat(1.0f), cb = hsplat(-1152.0f);
 #pragma unroll
   for (int i = 0; i < LB; i++) {
     if (i >= nb) break;
-    const uint32_t x0 = f.q[i].x ^ 0x80808080u, x1 = f.q[i].y ^ 0x80808080u;
-    const h8 b = mk_h8(pk_fma(perm(0x64646464u, x0, 0x04010400u), one, cb),
-                       pk_fma(perm(0x64646464u, x0, 0x04030402u), one, cb),
-                       pk_fma(perm(0x64646464u, x1, 0x04010400u), one, cb),
-                       pk_fma(perm(0x64646464u, x1, 0x04030402u), one, cb));
+    const h8 b = legacy_b(f, i, g);
     const A8<XT> a = load_a8<XT>(xr, k0 + 32 * i + 8 * g);
     const f4 c = mfma_x<XT>(a, b, f4{0, 0, 0, 0});
     const float d = f16_bits_to_f32(f.d[i]);

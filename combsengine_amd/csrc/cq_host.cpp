@@ -186,6 +186,14 @@ struct GvsArgs {
   int M, N, K, units, usplit;
   CqEpi epi;
 };
+struct LgArgs {
+  const void* w;
+  const void* x;
+  void* y;
+  long long row_bytes;
+  int M, N, K, blocks;
+  CqEpi epi;
+};
 struct DequantArgs {
   const void* w;
   float* out;
@@ -212,6 +220,7 @@ struct DeviceModule {
   hipFunction_t gemv2[kNumFormats][2][2] = {};  // K-quants only     // [format][y f16]
   hipFunction_t gemvd[kNumFormats][3][2] = {};  // K-quants only: [format][NT 1, 2, 4][y f16]
   hipFunction_t gemvs[kNumFormats][2] = {};  // K-quants only: [format][y f16]
+  hipFunction_t gemml[kNumFormats][2][2] = {};  // 32-value formats only: [format][NT - 1][y f16]
   hipFunction_t gemvr[2][4] = {};  // Q4_K rows split across lanes: [y f16][log2 activation pieces per thread]
   int cus = 0;                        // compute units of the device
 };
@@ -328,6 +337,17 @@ void load_module(DeviceModule& d, int dev) {
       }
   }
   for (int fi = 0; fi < kNumFormats; fi++) {
+    if (block_values(kFormats[fi]) != 32) continue;
+    for (int nt = 1; nt <= 2; nt++)
+      for (int yt = 0; yt < 2; yt++) {
+        snprintf(name, sizeof name, "cq_gemml_%s_n%d_y%s", fmt_name(kFormats[fi]), nt, yt ? "f16" : "f32");
+        if (get(&d.gemml[fi][nt - 1][yt], name) != hipSuccess) {
+          d.err = std::string("missing kernel ") + name;
+          return;
+        }
+      }
+  }
+  for (int fi = 0; fi < kNumFormats; fi++) {
     if (block_values(kFormats[fi]) != 256) continue;
     for (int yt = 0; yt < 2; yt++) {
       snprintf(name, sizeof name, "cq_gemvs_%s_y%s", fmt_name(kFormats[fi]), yt ? "f16" : "f32");
@@ -377,7 +397,7 @@ constexpr int kUnset = -1000000;
 struct Knobs {
   int gemv_waves, gemv1, gemv1k, gemv1_grid, gemv1_i8, gemv1_prefetch2, gemv1_span, gemv1_spread,
       gemv1_wave_major, gemv2, gemv2_wpc, gemvd, gvd_nt, gvd_waves, gemm_kernel, gemm_waves, gemm2_mt,
-      gemm2_nt, gemm2_split, gateup_fused, gemvr, gemvs, gemvs_split;
+      gemm2_nt, gemm2_split, gateup_fused, gemvr, gemvs, gemvs_split, gemml, gemml_nt;
 };
 Knobs g_knobs;
 std::once_flag g_knobs_once;
@@ -411,6 +431,8 @@ void read_knobs() {
   k.gemvr = env_int("COMBS_GEMVR", 1);
   k.gemvs = env_int("COMBS_GEMVS", 1);
   k.gemvs_split = env_int("COMBS_GEMVS_SPLIT", 0);
+  k.gemml = env_int("COMBS_GEMML", 1);
+  k.gemml_nt = env_int("COMBS_GEMML_NT", 0);
   g_knobs = k;
 }
 const Knobs& knobs() {
@@ -1017,6 +1039,36 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
   return CQ_OK;
 }
 
+// Prefill GEMM for the 32-value formats (cq_gemml_*, fp16 x): 4 waves x NT
+// 16-row weight tiles x 128 activation rows per workgroup, two workgroups
+// per compute unit; NT = 2 when the two-tile grid still has a workgroup per
+// compute unit (Q8_0 14336 x 4096: m = 128 71 us with one tile against 108
+// with two, m = 512 178 against 197, m = 2048 587 against 660).
+// COMBS_GEMML_NT forces it, COMBS_GEMML=0 keeps these formats on the 16-row
+// MFMA GEMV (m = 512: 3086 us).
+static cq_status launch_gemml(DeviceModule* dm, const cq_weight* w, const void* x, int64_t m, void* y, int yt,
+                              hipStream_t s, const CqEpi& epi) {
+  const int fi = fmt_index(w->format);
+  LgArgs a{};
+  a.w = w->dev;
+  a.x = x;
+  a.y = y;
+  a.row_bytes = (long long)(w->nbytes / (size_t)w->n);
+  a.M = (int)m;
+  a.N = (int)w->n;
+  a.K = (int)w->k;
+  a.blocks = (int)(w->k / 32);
+  a.epi = epi;
+  const long long mblk = (m + 127) / 128;
+  int nt = knobs().gemml_nt;
+  if (nt != 1 && nt != 2) nt = ((w->n + 127) / 128) * mblk >= dm->cus ? 2 : 1;
+  const long long gx = (w->n + 64 * nt - 1) / (64 * nt);
+  if (gx > 0x7fffffffLL || mblk > 65535) return fail(CQ_ERR_BAD_SHAPE, "grid too large");
+  void* params[] = {&a};
+  HIP_TRY(klaunch(dm, dm->gemml[fi][nt - 1][yt], (unsigned)gx, (unsigned)mblk, 1, 256, 0, s, params));
+  return CQ_OK;
+}
+
 // Prefill GEMM (cq_gemm_*, K-quants): workgroups of nw waves x 16 weight rows
 // and 64 (fp16 x) or 32 (fp32 x) activation rows.
 static cq_status launch_gemm(DeviceModule* dm, const cq_weight* w, const void* x, int xt, int64_t m, void* y, int yt,
@@ -1057,12 +1109,14 @@ static cq_status matmul_impl(const cq_weight* w, const void* x, int x_dtype, int
   cq_status st = device_module(&dm);
   if (st != CQ_OK) return st;
   const int xt = x_dtype == CQ_F32, yt = y_dtype == CQ_F16;
-  // Prefill GEMM for m > 16 on K-quants (or when forced); the GEMV kernel
-  // tiles m by 16 otherwise.  Legacy 32-value formats always use the GEMV
-  // kernel.
+  // Prefill GEMM for m > 16 (or when forced): cq_gemm2_* / cq_gemm_* for the
+  // K-quants, cq_gemml_* for the 32-value formats with fp16 x; the GEMV
+  // kernels tile m by 16 otherwise.
   const bool kq = block_values(w->format) == 256;
   if (kq && (path == CQ_PATH_GEMM || (path == CQ_PATH_AUTO && m > 16)))
     return launch_gemm(dm, w, x, xt, m, y, yt, (hipStream_t)stream, epi);
+  if (!kq && !xt && knobs().gemml && (path == CQ_PATH_GEMM || (path == CQ_PATH_AUTO && m > 16)))
+    return launch_gemml(dm, w, x, m, y, yt, (hipStream_t)stream, epi);
   if (m == 1 && !xt && path != CQ_PATH_GEMV && knobs().gemv1) {
     // quarter-superblock streaming kernel (cq_gemv2): COMBS_GEMV2=2 for
     // every K-quant, =1 for Q6_K, 0 (default) only where cq_gemv1 does not

@@ -1,11 +1,12 @@
 // Kernels of the library, compiled with hipcc --genco into one gfx950 code
 // object of four (cq_k_*.hip); the host library embeds all four and looks
 // each kernel up by its extern "C" name with hipModuleGetFunction.
-// This object: the prefill dequant-GEMMs (cq_gemm_*, cq_gemm2_*), the
+// This object: the prefill dequant-GEMMs (cq_gemm_*, cq_gemm2_*, cq_gemml_*), the
 // activation sub-block sums of their min term (cq_xsums_f16) and the split-K
 // reduction (cq_splitk_reduce_*).
 #include "cq_gemm.h"
 #include "cq_gemm2.h"
+#include "cq_gemml.h"
 
 #define GEMM_KERNEL(NAME, FMT, XT, YT)                                               \
   extern "C" __global__ void __launch_bounds__(512) NAME(const GemmArgs a) {         \
@@ -65,3 +66,20 @@ extern "C" __global__ void __launch_bounds__(256) cq_splitk_reduce_yf16(const fl
 extern "C" __global__ void __launch_bounds__(256) cq_xsums_f16(const _Float16* x, _Float16* xs, int M, int K) {
   xsums_body(x, xs, M, K);
 }
+
+// Prefill dequant-GEMM for the 32-value block formats (cq_gemml.h):
+// [format] x [NT 1, 2] x [y dtype]; two workgroups per compute unit.
+#define GEMML_KERNEL(NAME, FMT, YT, NT)                                                                     \
+  extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) NAME(const LgArgs a) { \
+    gemml_body<FMT, YT, NT, 4>(a);                                                                         \
+  }
+#define GEMML_FMT(fname, FMT)                          \
+  GEMML_KERNEL(cq_gemml_##fname##_n1_yf32, FMT, 0, 1)  \
+  GEMML_KERNEL(cq_gemml_##fname##_n1_yf16, FMT, 1, 1)  \
+  GEMML_KERNEL(cq_gemml_##fname##_n2_yf32, FMT, 0, 2)  \
+  GEMML_KERNEL(cq_gemml_##fname##_n2_yf16, FMT, 1, 2)
+GEMML_FMT(q4_0, CQ_Q4_0)
+GEMML_FMT(q5_0, CQ_Q5_0)
+GEMML_FMT(q8_0, CQ_Q8_0)
+GEMML_FMT(q4_1, CQ_Q4_1)
+GEMML_FMT(q5_1, CQ_Q5_1)

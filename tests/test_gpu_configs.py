@@ -41,6 +41,10 @@ CASES.append(("c3-Q6K-lm_head-128256x4096", F.Q6K, 128256, 4096, (1, 4, 16), "f3
 # config 4: chunked prefill, fp16 out
 CASES.append(("c4-Q4K-14336x4096", F.Q4K, 14336, 4096, (128, 512, 2048), "f16"))
 CASES.append(("c4-Q6K-4096x14336", F.Q6K, 4096, 14336, (128, 512, 2048), "f16"))
+# prefill of the legacy formats at the config-2 MLP shape (the reference's
+# tiled Q8_0 kernel, qmatmul.rs:481-527), fp16 out
+for _f in (F.Q8_0, F.Q4_0):
+    CASES.append((f"c2p-{_f.name}-14336x4096", _f, 14336, 4096, (128, 512), "f16"))
 # config 5: one Qwen2.5-7B decoder layer (V and down in Q6_K)
 for _name, _f, _n, _k in (("q", F.Q4K, 3584, 3584), ("k", F.Q4K, 512, 3584), ("v", F.Q6K, 512, 3584),
                           ("o", F.Q4K, 3584, 3584), ("gate", F.Q4K, 18944, 3584), ("up", F.Q4K, 18944, 3584),

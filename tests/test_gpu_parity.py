@@ -469,3 +469,30 @@ def test_gemv_batched_shared(cuda, monkeypatch, fmt, split, n, k, m):
     yb = torch.empty((m, n), device="cuda")
     w.matmul_bias_into(xd, torch.from_numpy(b).cuda(), yb)
     O.assert_close(yb.cpu().numpy(), expect.astype(np.float64) + b, 1e-3, "bias")
+
+
+@pytest.mark.parametrize("fmt", sorted(LEGACY))
+@pytest.mark.parametrize("nt", ["1", "2"])
+@pytest.mark.parametrize("n,k,m", [(300, 320, 17), (130, 4096, 64), (1000, 1056, 130), (70, 2048, 300)])
+def test_gemm_legacy_formats(cuda, monkeypatch, fmt, nt, n, k, m):
+    """Prefill GEMM for the 32-value formats (cq_gemml_*): 128-row activation
+    tiles (ragged m), 16-row weight tiles (ragged n), steps of four blocks
+    with a partial last step (k = 320, 1056), one or two weight tiles per
+    wave; fp32 and fp16 y and the bias epilogue, against the oracle."""
+    import torch
+    monkeypatch.setenv("COMBS_GEMML_NT", nt)
+    data = synth(fmt, n, k)
+    wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
+    w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
+    x = O.x_pattern(m, k, 11, 29, 14.0, 16.0).reshape(m, k)
+    expect = O.ref_matmul(x, wd)
+    xd = torch.from_numpy(x).cuda().half()
+    kern = L.path_name(w, xd, torch.empty((m, n), device="cuda"))
+    print(f"gemml {fmt.name} nt={nt} n={n} k={k} m={m} kernels={kern}", flush=True)
+    assert kern.startswith(f"cq_gemml_{fmt.name.lower()}_n{nt}")
+    O.assert_close(_run(w, x, torch.float16, torch.float32), expect, 1e-3, "y32")
+    O.assert_close(_run(w, x, torch.float16, torch.float16), expect, 1e-3, "y16")
+    b = np.linspace(-2, 2, n).astype(np.float32)
+    yb = torch.empty((m, n), device="cuda")
+    w.matmul_bias_into(xd, torch.from_numpy(b).cuda(), yb)
+    O.assert_close(yb.cpu().numpy(), expect.astype(np.float64) + b, 1e-3, "bias")

@@ -267,12 +267,13 @@ def empty_launch(dev):
 
 def llama3_token(dev, ms=(1, 16)):
     """Decode tokens/s of one Llama-3-8B token's projection set: 32 layers of
-    q [4096x4096], k and v [1024x4096], o [4096x4096] (Q4_K), the gated
-    gate/up pair [14336x4096] x 2 (one cq_matmul_gate_up call) and down
-    [4096x14336] (Q4_K), then the Q6_K lm_head [128256x4096]; every layer
-    has its own weight buffers (4.3 GB in all), the whole token is one
-    captured graph.  Only the projections are timed (no attention, norms or
-    sampling), so this is the projection-bound decode rate at batch m."""
+    q [4096x4096], k and v [1024x4096] (one cq_matmul_multi call over the
+    three), o [4096x4096] (Q4_K), the gated gate/up pair [14336x4096] x 2 (one
+    cq_matmul_gate_up call) and down [4096x14336] (Q4_K), then the Q6_K
+    lm_head [128256x4096]: four library calls per layer.  Every layer has its
+    own weight buffers (4.3 GB in all), the whole token is one captured
+    graph.  Only the projections are timed (no attention, norms or sampling),
+    so this is the projection-bound decode rate at batch m."""
     import torch
     from combsengine_amd import QuantFormat as F
     from combsengine_amd import QuantWeight
@@ -290,7 +291,6 @@ def llama3_token(dev, ms=(1, 16)):
     head = QuantWeight.from_device(F.Q6K, torch.from_numpy(hdata.copy()).to(dev), 128256, 4096)
     wbytes += hdata.size
     out = {"weight_bytes": wbytes, "layers": layers}
-    s = torch.cuda.current_stream().cuda_stream
     for m in ms:
         yt = torch.float32 if m == 1 else torch.float16
         x4 = torch.randn((m, 4096), device=dev).half()
@@ -299,12 +299,19 @@ def llama3_token(dev, ms=(1, 16)):
         yh = torch.empty((m, 128256), dtype=yt, device=dev)
         ydt = L.CQ_F16 if yt == torch.float16 else L.CQ_F32
 
+        import ctypes
+        qkv_w = [(ctypes.c_void_p * 3)(*[bufs[n][l].handle.value for n in ("q", "k", "v")]) for l in range(layers)]
+        qkv_y = (ctypes.c_void_p * 3)(*[ys[n].data_ptr() for n in ("q", "k", "v")])
+
         def token(_i):
             for l in range(layers):
-                for name in ("q", "k", "v", "o"):
-                    bufs[name][l].matmul_into(x4, ys[name])
+                st = L.lib().cq_matmul_multi(3, qkv_w[l], x4.data_ptr(), L.CQ_F16, m, qkv_y, ydt,
+                                             torch.cuda.current_stream().cuda_stream)
+                assert st == L.CQ_OK, L.last_error()
+                bufs["o"][l].matmul_into(x4, ys["o"])
                 st = L.lib().cq_matmul_gate_up(bufs["gate"][l].handle, bufs["up"][l].handle, x4.data_ptr(), L.CQ_F16,
-                                               m, L.CQ_ACT_SILU, ys["gate"].data_ptr(), ydt, s)
+                                               m, L.CQ_ACT_SILU, ys["gate"].data_ptr(), ydt,
+                                               torch.cuda.current_stream().cuda_stream)
                 assert st == L.CQ_OK, L.last_error()
                 bufs["down"][l].matmul_into(x14, ys["down"])
             head.matmul_into(x4, yh)
@@ -312,7 +319,7 @@ def llama3_token(dev, ms=(1, 16)):
         st = stats(replay_times(g, 1, 10))
         us = st["median"]
         out[f"m{m}"] = {"us_per_token_step": us, "tokens_per_s": round(m * 1e6 / us, 1),
-                        "weight_GBps": round(wbytes / us / 1e3, 1), "launches": layers * 6 + 1, "stats": st}
+                        "weight_GBps": round(wbytes / us / 1e3, 1), "library_calls": layers * 4 + 1, "stats": st}
     return out
 
 

@@ -9,6 +9,7 @@ reference's seam; the compute lives only in lib/libcombs_qlinear.so.
 """
 from .qlinear import (  # noqa: F401
     Activation, BadShape, Linear, ModelError, QuantFormat, QuantLinearOp, QuantTensor, QuantWeight, gated_up,
+    multi_forward,
     block_bytes, block_values, dequantize_gpu, quantize, tensor_byte_size, try_quant_linear,
 )
 from .gguf import GgufSource  # noqa: F401,E402

@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(HERE, "lib", "libcombs_qlinear.so")
 EXPORTS = (
     "cq_block_values", "cq_block_bytes", "cq_tensor_bytes", "cq_weight_create",
     "cq_weight_wrap_device", "cq_weight_destroy", "cq_weight_dims", "cq_weight_vram_bytes",
-    "cq_weight_device_ptr", "cq_matmul", "cq_matmul_path", "cq_matmul_bias", "cq_matmul_gate_up",
+    "cq_weight_device_ptr", "cq_matmul", "cq_matmul_path", "cq_matmul_bias", "cq_matmul_gate_up", "cq_matmul_multi",
     "cq_dequantize", "cq_quantize", "cq_matmul_kernels", "cq_reload_options", "cq_matmul_noalloc",
     "cq_device_init",
     "cq_last_error", "cq_version",
@@ -56,6 +56,7 @@ def lib():
         "cq_matmul_path": ([P, P, i32, i64, P, i32, i32, P], i32),
         "cq_matmul_bias": ([P, P, i32, i64, P, i32, P, i32, P], i32),
         "cq_matmul_gate_up": ([P, P, P, i32, i64, i32, P, i32, P], i32),
+        "cq_matmul_multi": ([i32, P, P, i32, i64, P, i32, P], i32),
         "cq_dequantize": ([i32, P, sz, i64, P, P], i32),
         "cq_quantize": ([i32, P, i64, i64, P, sz, i32], i32),
         "cq_matmul_kernels": ([P, i32, i64, i32, ctypes.c_char_p, sz], i32),

@@ -55,7 +55,17 @@ struct Gv1Args {
   int wave_major;       // 1: task t runs on wave t / grid of workgroup t % grid (balanced), 0: on workgroup t / NW
   int span;             // 1: load each task as a contiguous span (formats with whole 16-byte units)
   CqEpi epi;
+  // EPI = 3: up to GV1_MSEG weights of one format and K against the same
+  // activation row, one output each; task t belongs to weight i when
+  // mt0[i] <= t < mt0[i + 1] (each weight's rows a multiple of R, so no task
+  // straddles two)
+  const uint8_t* mw[4];
+  void* my[4];
+  int mt0[5];
+  int mn[4];
+  int nseg;
 };
+#define GV1_MSEG 4
 
 __shared__ __attribute__((aligned(16))) int8_t gv_xh[GV1_XMAX / 256 * GV1_XSTRIDE];
 __shared__ __attribute__((aligned(16))) int8_t gv_xl[GV1_XMAX / 256 * GV1_XSTRIDE];
@@ -661,9 +671,12 @@ template <int FMT, int EPI>
 constexpr int gv1_kernel_waves() {
   return EPI == 2 && FMT == CQ_Q6_K ? 4 : gv1_waves<FMT>();
 }
+// EPI = 3: several weights against one activation row (Gv1Args::mw / my),
+// fp16-register path only.
 template <int FMT, int YT, int EPI, int NW = gv1_kernel_waves<FMT, EPI>(),
           int XM = (EPI == 2 && FMT == CQ_Q6_K) ? 0 : gv1_xmode<FMT>()>
 __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
+  static_assert(EPI != 3 || XM == 1, "several weights per launch: fp16-register path only");
   constexpr int BB = gv1_unit_bytes<FMT>();
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -704,9 +717,9 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
   };
   Gv3XRegs xregs;  // XM = 1 only
   // Row sums across the lanes of each row, then the store (and epilogue).
-  auto task_store = [&](float part, int tt) {
+  auto task_store = [&](float part, int tt, void* yv, int N) {
     const int r0 = tt * (EPI == 2 ? half : a.rows);
-    const int nrows = min(EPI == 2 ? half : a.rows, a.N - r0);
+    const int nrows = min(EPI == 2 ? half : a.rows, N - r0);
     const int rq = EPI == 2 && myrow >= half ? myrow - half : myrow;  // output row of this lane
     if ((a.units & (a.units - 1)) == 0) {
       // a row's lanes form an aligned group of `units` lanes: butterfly within it
@@ -715,10 +728,10 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
         // up row rq sits half * units lanes after its gate row
         const float upv = __shfl(part, (lane + half * a.units) & 63, 64);
         if (myunit == 0 && myrow < half && rq < nrows)
-          cq_store_raw<YT>(a.y, cq_gated<YT>(part, upv, a.epi.act), r0 + rq);
+          cq_store_raw<YT>(yv, cq_gated<YT>(part, upv, a.epi.act), r0 + rq);
       } else if (myunit == 0 && myrow < nrows) {
-        if constexpr (EPI == 1) cq_store<YT>(a.y, a.epi, part, r0 + myrow, r0 + myrow);
-        else cq_store_raw<YT>(a.y, part, r0 + myrow);
+        if constexpr (EPI == 1) cq_store<YT>(yv, a.epi, part, r0 + myrow, r0 + myrow);
+        else cq_store_raw<YT>(yv, part, r0 + myrow);
       }
     } else if constexpr (EPI == 2) {
       // gate row q and its up row q + half, each summed over the wave
@@ -729,7 +742,7 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
           v += __shfl_xor(v, o, 64);
           u += __shfl_xor(u, o, 64);
         }
-        if (lane == 0 && q < nrows) cq_store_raw<YT>(a.y, cq_gated<YT>(v, u, a.epi.act), r0 + q);
+        if (lane == 0 && q < nrows) cq_store_raw<YT>(yv, cq_gated<YT>(v, u, a.epi.act), r0 + q);
       }
     } else {
       for (int q = 0; q < a.rows; q++) {
@@ -737,8 +750,8 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
         if (lane == 0 && q < nrows) {
-          if constexpr (EPI == 1) cq_store<YT>(a.y, a.epi, v, r0 + q, r0 + q);
-          else cq_store_raw<YT>(a.y, v, r0 + q);
+          if constexpr (EPI == 1) cq_store<YT>(yv, a.epi, v, r0 + q, r0 + q);
+          else cq_store_raw<YT>(yv, v, r0 + q);
         }
       }
     }
@@ -773,7 +786,7 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
       else part = gv1_superblock<FMT>(blk, xh, xl, xe, gv_xs + 8 * myunit, gv_s + 8 * myunit);
       }
     }
-    task_store(part, tt);
+    task_store(part, tt, a.y, a.N);
   };
   // Load order matters (the vector-memory counter retires in order): the
   // activation chunks first, then the first task's weights, so that staging
@@ -802,6 +815,22 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
     __shared__ __attribute__((aligned(16))) u4v gv_sb[NW * SP];
     static_assert(NW * SP * 16 >= GV1_XMAX / 256 * 528, "the staged row fits in gv_sb");
     const int n = t < a.tasks ? (a.tasks - 1 - t) / stride + 1 : 0;
+    // task tt -> (weight, output, rows, task within the weight): the launch's
+    // own for EPI != 3, weight i's for EPI = 3 (uniform over the wave)
+    struct View {
+      const uint8_t* w;
+      void* y;
+      int N, t;
+    };
+    auto view = [&](int tt) -> View {
+      if constexpr (EPI == 3) {
+        int i = 0;
+#pragma unroll
+        for (int q = 1; q < GV1_MSEG; q++) i += (q < a.nseg && tt >= a.mt0[q]) ? 1 : 0;
+        return View{a.mw[i], a.my[i], a.mn[i], tt - a.mt0[i]};
+      }
+      return View{a.w, a.y, a.N, tt};
+    };
     auto dma_task = [&](u4v* arr, int tt) {
       const uint8_t *b0, *b1;
       int seg, lim0, lim1;
@@ -811,8 +840,9 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
         const size_t off = (size_t)r0 * a.units * BB;
         b0 = a.w + off, b1 = a.w2 + off, seg = half * a.units * (BB / 16), lim0 = lim1 = lim;
       } else {
-        const int r0 = tt * a.rows, lim = (min(a.rows, a.N - r0) * a.units * BB + 15) / 16;
-        b0 = b1 = a.w + (size_t)r0 * a.units * BB, seg = 1 << 30, lim0 = lim1 = lim;
+        const View v = view(tt);
+        const int r0 = v.t * a.rows, lim = (min(a.rows, v.N - r0) * a.units * BB + 15) / 16;
+        b0 = b1 = v.w + (size_t)r0 * a.units * BB, seg = 1 << 30, lim0 = lim1 = lim;
       }
       u4v* dst = arr + wave * SP;
 #pragma unroll
@@ -823,8 +853,9 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
       }
     };
     auto compute = [&](const u4v* arr, int tt) {
-      const int r0 = tt * (EPI == 2 ? half : a.rows);
-      const int nrows = min(EPI == 2 ? half : a.rows, a.N - r0);
+      const View v = view(tt);
+      const int r0 = v.t * (EPI == 2 ? half : a.rows);
+      const int nrows = min(EPI == 2 ? half : a.rows, v.N - r0);
       const int rq = EPI == 2 && myrow >= half ? myrow - half : myrow;
       float part = 0.0f;
       if (lane < lanes_used && rq < nrows) {
@@ -834,7 +865,7 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
         else if constexpr (FMT == CQ_Q5_K) part = gv3_superblock_q5k((const u4v*)sbp, xregs);
         else part = gv3_unit_legacy<FMT>(sbp, xregs);
       }
-      task_store(part, tt);
+      task_store(part, v.t, v.y, v.N);
     };
     // The activation row (K fp16, a multiple of 8 values) goes to gv_sb by
     // DMA with each 256-value unit at a 264-value (528-byte) stride: units

@@ -143,6 +143,7 @@ struct LtArgs {
   int M, N, K, units, usplit;
   CqEpi epi;
 };
+constexpr int kMultiMax = 4;  // weights per cq_matmul_multi launch (GV1_MSEG)
 struct Gv1Args {
   const void* w;
   const void* w2;
@@ -151,6 +152,11 @@ struct Gv1Args {
   long long row_bytes;
   int N, K, units, rows, tasks, prefetch2, wave_major, span;
   CqEpi epi;
+  const void* mw[kMultiMax];
+  void* my[kMultiMax];
+  int mt0[kMultiMax + 1];
+  int mn[kMultiMax];
+  int nseg;
 };
 struct Gv2Args {
   const void* w;
@@ -215,6 +221,7 @@ struct DeviceModule {
   hipFunction_t xsums = nullptr;
   hipFunction_t reduce[2] = {};       // split-K epilogue [y f16]
   hipFunction_t gemv1[kNumFormats][2][3] = {};  // [format][y f16][epilogue: none, general, gated]
+  hipFunction_t gemv1_multi[kNumFormats][2] = {};  // several weights, one row: [format][y f16]
   hipFunction_t gemv1_i8[kNumFormats][2][2] = {};
   hipFunction_t gemv1k[kNumFormats][2][2] = {};   // rows of 65-128 units, Q4_K / Q5_K / Q6_K / Q4_0 [format][y f16][epilogue]
   hipFunction_t gemv2[kNumFormats][2][2] = {};  // K-quants only     // [format][y f16]
@@ -305,6 +312,13 @@ void load_module(DeviceModule& d, int dev) {
           return;
         }
         const int f = kFormats[fi];
+        if (ep == 0 && (f == CQ_Q4_K || f == CQ_Q5_K || f == CQ_Q6_K || f == CQ_Q4_0 || f == CQ_Q8_0)) {
+          snprintf(name, sizeof name, "cq_gemv1_%s_y%s_multi", fmt_name(f), yt ? "f16" : "f32");
+          if (get(&d.gemv1_multi[fi][yt], name) != hipSuccess) {
+            d.err = std::string("missing kernel ") + name;
+            return;
+          }
+        }
         if (ep < 2 && (f == CQ_Q4_K || f == CQ_Q4_0 || f == CQ_Q8_0)) {
           snprintf(name, sizeof name, "cq_gemv1_%s_y%s%s_i8", fmt_name(f), yt ? "f16" : "f32", ep ? "_epi" : "");
           if (get(&d.gemv1_i8[fi][yt][ep], name) != hipSuccess) {
@@ -397,7 +411,7 @@ constexpr int kUnset = -1000000;
 struct Knobs {
   int gemv_waves, gemv1, gemv1k, gemv1_grid, gemv1_i8, gemv1_prefetch2, gemv1_span, gemv1_spread,
       gemv1_wave_major, gemv2, gemv2_wpc, gemvd, gvd_nt, gvd_waves, gemm_kernel, gemm_waves, gemm2_mt,
-      gemm2_nt, gemm2_split, gateup_fused, gemvr, gemvs, gemvs_split, gemml, gemml_nt;
+      gemm2_nt, gemm2_split, gateup_fused, gemvr, gemvs, gemvs_split, gemml, gemml_nt, multi_fused;
 };
 Knobs g_knobs;
 std::once_flag g_knobs_once;
@@ -433,6 +447,7 @@ void read_knobs() {
   k.gemvs_split = env_int("COMBS_GEMVS_SPLIT", 0);
   k.gemml = env_int("COMBS_GEMML", 1);
   k.gemml_nt = env_int("COMBS_GEMML_NT", 0);
+  k.multi_fused = env_int("COMBS_MULTI_FUSED", 1);
   g_knobs = k;
 }
 const Knobs& knobs() {
@@ -846,11 +861,13 @@ static bool gemv1_gated_fits(const cq_weight* gate, const cq_weight* up) {
   return gemv1_fits(gate) && gemv1_fits(up) && gate->k / 256 <= 32;
 }
 // gated (up != null): y = act(x . W^T) * (x . up^T) in one launch; needs
-// K / 256 up to 32 (gemv1_gated_fits).
+// K / 256 up to 32 (gemv1_gated_fits).  multi (count > 0): weights ws[0 ..
+// count) against x into ys[i], one launch (w = ws[0]).
 static cq_status launch_gemv1(DeviceModule* dm, const cq_weight* w, const void* x, void* y, int yt, hipStream_t s,
-                              const CqEpi& epi, const cq_weight* up = nullptr) {
+                              const CqEpi& epi, const cq_weight* up = nullptr, int count = 0,
+                              const cq_weight* const* ws = nullptr, void* const* ys = nullptr) {
   const int fi = fmt_index(w->format);
-  Gv1Args a;
+  Gv1Args a{};
   a.w = w->dev;
   a.w2 = up ? up->dev : nullptr;
   a.x = x;
@@ -862,11 +879,25 @@ static cq_status launch_gemv1(DeviceModule* dm, const cq_weight* w, const void* 
   a.rows = a.units >= 64 ? 1 : 64 / a.units;
   const int per_task = up ? a.rows / 2 : a.rows;
   a.tasks = (int)((w->n + per_task - 1) / per_task);
+  if (count > 0) {
+    int t0 = 0;
+    for (int i = 0; i < count; i++) {
+      a.mw[i] = ws[i]->dev;
+      a.my[i] = ys[i];
+      a.mn[i] = (int)ws[i]->n;
+      a.mt0[i] = t0;
+      t0 += (int)(ws[i]->n / a.rows);  // (a multiple of R, checked by the caller)
+    }
+    a.mt0[count] = t0;
+    a.nseg = count;
+    a.tasks = t0;
+    a.N = t0 * a.rows;
+  }
   a.prefetch2 = knobs().gemv1_prefetch2;
   a.span = knobs().gemv1_span;
   a.wave_major = knobs().gemv1_wave_major;
   a.epi = epi;
-  const int ep = up ? 2 : (epi.bias || epi.aux) ? 1 : 0;
+  const int ep = count > 0 ? 3 : up ? 2 : (epi.bias || epi.aux) ? 1 : 0;
   // Weights with fewer workgroups of tasks than compute units spread their
   // tasks over every compute unit, wave-major (task t on wave t / grid of
   // workgroup t % grid): workgroup-major packing left most compute units
@@ -876,7 +907,7 @@ static cq_status launch_gemv1(DeviceModule* dm, const cq_weight* w, const void* 
   // 4096: 5.5 / 7.2 against 5.8 / 7.5 us); with at most one task per
   // workgroup, and for Q4_K, the register path is faster.  COMBS_GEMV1_I8:
   // 0 never, 2 whenever the weight is small.
-  hipFunction_t k = dm->gemv1[fi][yt][ep];
+  hipFunction_t k = ep == 3 ? dm->gemv1_multi[fi][yt] : dm->gemv1[fi][yt][ep];
   int nw = gemv1_waves(w->format, up != nullptr);
   int cap = knobs().gemv1_grid != kUnset ? knobs().gemv1_grid : dm->cus;
   if (cap < 1) cap = 1;
@@ -1191,6 +1222,40 @@ cq_status cq_matmul_gate_up(const cq_weight* gate, const cq_weight* up, const vo
   epi.aux_f16 = y_dtype == CQ_F16;
   epi.act = act;
   return matmul_impl(gate, x, x_dtype, m, y, y_dtype, CQ_PATH_AUTO, stream, epi);
+}
+
+// Several projections of one input: one launch of cq_gemv1's multi-weight
+// kernel for decode (m = 1, fp16 x, one format on the fp16-register path,
+// every weight's rows a multiple of the rows per task), else one cq_matmul
+// per weight.  COMBS_MULTI_FUSED=0 always takes the separate launches.
+cq_status cq_matmul_multi(int count, const cq_weight* const* ws, const void* x, int x_dtype, int64_t m,
+                          void* const* ys, int y_dtype, void* stream) {
+  if (count < 1 || count > kMultiMax) return fail(CQ_ERR_BAD_SHAPE, "count %d outside 1..%d", count, kMultiMax);
+  if (!ws || !ys || !x) return fail(CQ_ERR_NULL, "NULL weights, outputs or x");
+  for (int i = 0; i < count; i++) {
+    if (!ws[i] || !ys[i]) return fail(CQ_ERR_NULL, "NULL weight or output %d", i);
+    if (ws[i]->k != ws[0]->k)
+      return fail(CQ_ERR_BAD_SHAPE, "weight %d has k=%lld, weight 0 k=%lld", i, (long long)ws[i]->k,
+                  (long long)ws[0]->k);
+  }
+  bool one = m == 1 && x_dtype == CQ_F16 && knobs().multi_fused && (y_dtype == CQ_F16 || y_dtype == CQ_F32);
+  const int f = ws[0]->format;
+  one = one && (f == CQ_Q4_K || f == CQ_Q5_K || f == CQ_Q6_K || f == CQ_Q4_0 || f == CQ_Q8_0);
+  const int64_t units = ws[0]->k / 256;
+  const int64_t rows = units >= 64 ? 1 : 64 / (units > 0 ? units : 1);
+  for (int i = 0; one && i < count; i++)
+    one = ws[i]->format == f && gemv1_fits(ws[i]) && ws[i]->n % rows == 0;
+  if (one) {
+    DeviceModule* dm;
+    cq_status st = device_module(&dm);
+    if (st != CQ_OK) return st;
+    return launch_gemv1(dm, ws[0], x, ys[0], y_dtype == CQ_F16, (hipStream_t)stream, CqEpi{}, nullptr, count, ws, ys);
+  }
+  for (int i = 0; i < count; i++) {
+    const cq_status st = matmul_impl(ws[i], x, x_dtype, m, ys[i], y_dtype, CQ_PATH_AUTO, stream, CqEpi{});
+    if (st != CQ_OK) return st;
+  }
+  return CQ_OK;
 }
 
 cq_status cq_matmul(const cq_weight* w, const void* x, int x_dtype, int64_t m, void* y, int y_dtype, void* stream) {

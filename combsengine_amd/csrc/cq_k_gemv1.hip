@@ -25,6 +25,16 @@ GEMV1_FMT(q4_1, CQ_Q4_1)
 GEMV1_FMT(q5_0, CQ_Q5_0)
 GEMV1_FMT(q5_1, CQ_Q5_1)
 GEMV1_FMT(q8_0, CQ_Q8_0)
+// Several weights of one format and K against one activation row (the
+// projections that share an input, e.g. q / k / v), fp16-register path.
+#define GEMV1_MULTI_FMT(fname, FMT)                     \
+  GEMV1_KERNEL(cq_gemv1_##fname##_yf32_multi, FMT, 0, 3) \
+  GEMV1_KERNEL(cq_gemv1_##fname##_yf16_multi, FMT, 1, 3)
+GEMV1_MULTI_FMT(q4_k, CQ_Q4_K)
+GEMV1_MULTI_FMT(q5_k, CQ_Q5_K)
+GEMV1_MULTI_FMT(q6_k, CQ_Q6_K)
+GEMV1_MULTI_FMT(q4_0, CQ_Q4_0)
+GEMV1_MULTI_FMT(q8_0, CQ_Q8_0)
 // The int8 activation path for Q4_K, Q4_0 and Q8_0, whose default is the
 // register path: cheaper to set up, chosen by the host when every wave has
 // at most one task (small weights: 4096 x 4096 Q4_0 5.6 against 6.7 us;

@@ -303,6 +303,27 @@ def gated_up(activation, gate: "QuantLinearOp", up: "QuantLinearOp", h):
     return y.reshape(b, s, n).to(h.dtype)
 
 
+def multi_forward(ops, h):
+    """[op.forward(h) for op in ops] (the q / k / v projections of one input,
+    llama.rs:261-263) as one library call (cq_matmul_multi): for decode a
+    single launch streams every weight.  h [batch, seq, k] fp16/fp32 (other
+    float dtypes through fp32) -> list of [batch, seq, n_i] in h's dtype."""
+    torch = _torch()
+    b, s, k = h.shape
+    if not 1 <= len(ops) <= 4 or any(op.dims()[1] != k for op in ops):
+        raise BadShape("multi input", [len(ops), k], [op.dims() for op in ops])
+    x = _kernel_input(h).reshape(b * s, k).contiguous()
+    ys = [torch.empty((b * s, op.dims()[0]), dtype=x.dtype, device=h.device) for op in ops]
+    for op, y in zip(ops, ys):
+        op.w._io(x, y)
+    xt = _XT[str(x.dtype)]
+    wa = (ctypes.c_void_p * len(ops))(*[op.w.handle.value for op in ops])
+    ya = (ctypes.c_void_p * len(ops))(*[y.data_ptr() for y in ys])
+    st = L.lib().cq_matmul_multi(len(ops), wa, x.data_ptr(), xt, b * s, ya, xt, _stream_ptr(x.device))
+    _check(st, "cq_matmul_multi", "multi input", [b * s, k], list(x.shape))
+    return [y.reshape(b, s, -1).to(h.dtype) for y in ys]
+
+
 class Linear:
     """enum Linear { Dense(Tensor), Quant(Box<dyn QuantLinearOp>) }
     (qlinear.rs:67-99).  The bias is added outside the op."""

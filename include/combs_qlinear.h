@@ -134,6 +134,15 @@ typedef enum { CQ_ACT_SILU = 0, CQ_ACT_GELU_TANH = 1, CQ_ACT_GELU = 2 } cq_act;
 cq_status cq_matmul_gate_up(const cq_weight* gate, const cq_weight* up, const void* x, int x_dtype, int64_t m,
                             int act, void* y, int y_dtype, void* stream);
 
+/* Several projections of one input: ys[i][m, n_i] = x[m,k] . dequant(ws[i])^T
+ * for i < count (1..4), every weight with the same k.  Replaces consecutive
+ * QuantLinearOp::forward calls on one activation, as the attention block's
+ * q / k / v projections (llama.rs:261-263).  Decode (m = 1, fp16 x) of
+ * weights of one format streams all of them in a single launch; otherwise
+ * one cq_matmul per weight, in order, on `stream`. */
+cq_status cq_matmul_multi(int count, const cq_weight* const* ws, const void* x, int x_dtype, int64_t m,
+                          void* const* ys, int y_dtype, void* stream);
+
 /* Bit-exact dequantisation of a device block stream to f32 (validation).
  * Replaces dequantize_*_gpu (qmatmul.rs:171-190, 530-573, 1232-1305); the
  * result equals gguf.rs dequantize_* (gguf.rs:755-999) bit for bit. */

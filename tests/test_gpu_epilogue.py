@@ -229,3 +229,31 @@ def test_gate_up_single_row_one_launch(cuda, monkeypatch, fmt, n, k, fused, y_dt
     assert st == L.CQ_OK, L.last_error()
     torch.cuda.synchronize()
     O.assert_close(y.float().cpu().numpy(), expect, 1e-3 if y_dt == "f32" else 2e-3)
+
+
+@pytest.mark.parametrize("fmt", [QuantFormat.Q4K, QuantFormat.Q5K, QuantFormat.Q6K, QuantFormat.Q4_0,
+                                 QuantFormat.Q8_0, QuantFormat.Q5_0])
+@pytest.mark.parametrize("ns,k", [((4096, 1024, 1024), 4096), ((512, 128, 128, 64), 1024), ((300, 36), 2304),
+                                  ((96,), 16384), ((3584, 512, 512), 3584)])
+@pytest.mark.parametrize("m", [1, 3])
+def test_matmul_multi(cuda, monkeypatch, fmt, ns, k, m):
+    """Several projections of one input (q / k / v, llama.rs:261-263): one
+    launch for decode where every weight's rows fill whole tasks (fp16-register
+    formats), else one call per weight (m = 3, Q5_0, row counts that do not
+    divide the task); each output against the oracle, and equal to the
+    separate launches (COMBS_MULTI_FUSED=0) to the same bar."""
+    import torch
+    from combsengine_amd import multi_forward
+    ws = [_weight(fmt, n, k, 60 + i + int(fmt)) for i, n in enumerate(ns)]
+    x = _x(m, k, 61)
+    h = torch.from_numpy(x).cuda().half().reshape(1, m, k)
+    ops = [QuantLinearOp(w) for _, w in ws]
+    print(f"multi {fmt.name} ns={ns} k={k} m={m} kernels={L.kernels(ws[0][1], L.CQ_F16, m, L.CQ_F16)}", flush=True)
+    ys = multi_forward(ops, h)
+    monkeypatch.setenv("COMBS_MULTI_FUSED", "0")
+    ys_sep = multi_forward(ops, h)
+    for (data, w), n, y, ysep in zip(ws, ns, ys, ys_sep):
+        assert y.shape == (1, m, n) and y.dtype == torch.float16
+        expect = O.fused_matmul(int(fmt), data, x, n, k)
+        O.assert_close(y.float().cpu().numpy().reshape(m, n), expect, 2e-3, f"n={n}")
+        O.assert_close(y.float().cpu().numpy(), ysep.float().cpu().numpy(), 2e-3, f"n={n} vs separate")

@@ -350,6 +350,18 @@ def secondary(dev):
                           "frac_fp16_peak": round(fl / us_g / 1e6 / FP16_PEAK_TFLOPS, 4), "stats": st_g},
                 "kernels": L.kernels(pool[0], L.CQ_F16, m, L.CQ_F16)}
         del pool
+    # prefill of a 32-value block format (the reference's tiled Q8_0 kernel,
+    # qmatmul.rs:481-527) at the Llama-3-8B MLP shape, eager, fp16 out
+    pool, data = make_pool(QuantFormat.Q8_0, 14336, 4096, 0.3 * (1 << 30), seed=330)
+    for m in (128, 512):
+        x = torch.from_numpy(rng.normal(0, 1, (m, 4096)).astype(np.float16)).to(dev)
+        y = torch.empty((m, 14336), dtype=torch.float16, device=dev)
+        us_e, st_e = eager_time_us(fast_launcher(pool, x, y), 16, reps=7)
+        fl = 2.0 * m * 14336 * 4096
+        out[f"prefill_legacy_Q8_0_14336x4096_m{m}"] = {
+            "us": us_e, "TFLOPs": round(fl / us_e / 1e6, 1), "frac_fp16_peak": round(fl / us_e / 1e6 / FP16_PEAK_TFLOPS, 4),
+            "stats": st_e, "kernels": L.kernels(pool[0], L.CQ_F16, m, L.CQ_F16)}
+    del pool
     # lm_head Q6_K [128256 x 4096] (431 MB: larger than the Infinity Cache)
     pool, data = make_pool(QuantFormat.Q6K, 128256, 4096, 2 * 431e6, seed=77)
     x = torch.from_numpy(rng.normal(0, 1, (1, 4096)).astype(np.float16)).to(dev)
@@ -543,7 +555,7 @@ def main():
         extra.update(secondary(dev))
     if not args.no_extra and not args.no_configs:
         extra["configs"] = configs_2_3_5(dev)
-    prefill = {k: v for k, v in extra.items() if k.startswith("prefill_")}
+    prefill = {k: v for k, v in extra.items() if k.startswith("prefill_") and "eager" in v}
     best_prefill = max((v["eager"]["TFLOPs"] for v in prefill.values()), default=None)
     tok = extra.get("llama3_8b_decode_token", {}).get("m1", {})
 

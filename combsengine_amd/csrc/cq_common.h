@@ -56,6 +56,29 @@ __device__ __forceinline__ uint32_t bfi(uint32_t mask, uint32_t a, uint32_t b) {
 // rotate right (v_alignbit_b32)
 __device__ __forceinline__ uint32_t rotr(uint32_t v, uint32_t s) { return __builtin_amdgcn_alignbit(v, v, s); }
 
+// A lane's float from another lane of its 16-lane row, by a DPP modifier on
+// a VALU move (no LDS round trip, unlike __shfl_xor's ds_bpermute, whose
+// latency a reduction chain pays once per step).  CTRL: 0xB1 lane ^ 1,
+// 0x4E lane ^ 2 (quad permutes), 0x141 the mirror within each 8 lanes, 0x140
+// the mirror within the 16-lane row.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+// Sum over each aligned group of G lanes (G a power of two, 1..64, uniform);
+// every lane of a group gets the same value: within 16 lanes by DPP (pairs,
+// then quads, then the mirrors, which pair each lane with one of the other
+// half's, all of whose lanes hold that half's sum), across rows by shuffles.
+__device__ __forceinline__ float lane_group_sum(float v, int G) {
+  if (G >= 2) v += dpp_f32<0xB1>(v);
+  if (G >= 4) v += dpp_f32<0x4E>(v);
+  if (G >= 8) v += dpp_f32<0x141>(v);
+  if (G >= 16) v += dpp_f32<0x140>(v);
+  if (G >= 32) v += __shfl_xor(v, 16, 64);
+  if (G >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
 __device__ __forceinline__ h2 as_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
 __device__ __forceinline__ uint32_t as_u32(h2 v) { return __builtin_bit_cast(uint32_t, v); }
 __device__ __forceinline__ h2 hsplat(float v) {

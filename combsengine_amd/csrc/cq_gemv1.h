@@ -42,6 +42,13 @@
 #define GV1_XMAX 16384                       // largest K staged
 #define GV1_XSTRIDE 272                      // bytes per staged 256-value unit (16 pad)
 
+// Timeline hook of the fp16-register path: measurement builds define it to
+// record a timestamp per wave at each numbered point; the library build
+// compiles it to nothing.
+#ifndef GV1_MARK
+#define GV1_MARK(ev)
+#endif
+
 struct Gv1Args {
   const uint8_t* w;
   const uint8_t* w2;    // EPI = 2: the up projection (same format and shape as w, the gate)
@@ -722,8 +729,8 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
     const int nrows = min(EPI == 2 ? half : a.rows, N - r0);
     const int rq = EPI == 2 && myrow >= half ? myrow - half : myrow;  // output row of this lane
     if ((a.units & (a.units - 1)) == 0) {
-      // a row's lanes form an aligned group of `units` lanes: butterfly within it
-      for (int o = a.units >> 1; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+      // a row's lanes form an aligned group of `units` lanes: sum within it
+      part = lane_group_sum(part, a.units);
       if constexpr (EPI == 2) {
         // up row rq sits half * units lanes after its gate row
         const float upv = __shfl(part, (lane + half * a.units) & 63, 64);
@@ -736,19 +743,13 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
     } else if constexpr (EPI == 2) {
       // gate row q and its up row q + half, each summed over the wave
       for (int q = 0; q < half; q++) {
-        float v = myrow == q ? part : 0.0f, u = myrow == q + half ? part : 0.0f;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-          v += __shfl_xor(v, o, 64);
-          u += __shfl_xor(u, o, 64);
-        }
+        const float v = lane_group_sum(myrow == q ? part : 0.0f, 64);
+        const float u = lane_group_sum(myrow == q + half ? part : 0.0f, 64);
         if (lane == 0 && q < nrows) cq_store_raw<YT>(yv, cq_gated<YT>(v, u, a.epi.act), r0 + q);
       }
     } else {
       for (int q = 0; q < a.rows; q++) {
-        float v = myrow == q ? part : 0.0f;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+        const float v = lane_group_sum(myrow == q ? part : 0.0f, 64);
         if (lane == 0 && q < nrows) {
           if constexpr (EPI == 1) cq_store<YT>(yv, a.epi, v, r0 + q, r0 + q);
           else cq_store_raw<YT>(yv, v, r0 + q);
@@ -861,7 +862,15 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
       if (lane < lanes_used && rq < nrows) {
         const uint8_t* sbp = (const uint8_t*)(arr + wave * SP) + BB * lane;
         if constexpr (FMT == CQ_Q6_K) part = gv3_superblock_q6k(sbp, xregs);
-        else if constexpr (FMT == CQ_Q4_K) part = gv3_superblock_q4k((const u4v*)sbp, xregs);
+        else if constexpr (FMT == CQ_Q4_K) {
+          // all nine reads first: one LDS latency per superblock instead of
+          // one per group of reads the scheduler would interleave
+          u4v sb[9];
+#pragma unroll
+          for (int q = 0; q < 9; q++) sb[q] = ((const u4v*)sbp)[q];
+          __builtin_amdgcn_sched_barrier(0);
+          part = gv3_superblock_q4k(sb, xregs);
+        }
         else if constexpr (FMT == CQ_Q5_K) part = gv3_superblock_q5k((const u4v*)sbp, xregs);
         else part = gv3_unit_legacy<FMT>(sbp, xregs);
       }
@@ -873,6 +882,7 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
     // unit in one LDS bank.  A unit is one half-wave instruction (32 lanes x
     // 16 bytes); waves take unit pairs in turn.  These DMAs are the older
     // ones in the counter.
+    GV1_MARK(0);
     _Float16* x16p = (_Float16*)gv_sb;
     {
       const int nunits = a.K / 256;
@@ -884,13 +894,17 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
     }
     dma_task(gv_sa, min(t, a.tasks - 1));
     gv3_wait_vm<NI>();
+    GV1_MARK(1);
     __syncthreads();
+    GV1_MARK(7);
     xregs.load(myunit, x16p);
     xregs.lane_sums<FMT == CQ_Q6_K ? 16 : 32>();  // (Q4_K / legacy: 32-value blocks)
+    GV1_MARK(8);
     // The staged row (in gv_sb) fully read before any DMA into gv_sb.  (The
     // second task's DMA goes out only now: issued together with the first,
     // the headline shape measured 11.6 against 10.4 us.)
     __syncthreads();
+    GV1_MARK(2);
     for (int j = 0; j < n; j += 2, t += 2 * stride) {
       if (j + 1 < n) {
         dma_task(gv_sb, t + stride);
@@ -898,7 +912,9 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
       } else {
         gv3_wait_vm<0>();
       }
+      GV1_MARK(3 + 2 * j);
       compute(gv_sa, t);
+      GV1_MARK(4 + 2 * j);
       if (j + 1 >= n) break;
       if (j + 2 < n) {
         dma_task(gv_sa, t + 2 * stride);
@@ -906,7 +922,9 @@ __device__ __forceinline__ void gemv1_body(const Gv1Args& a) {
       } else {
         gv3_wait_vm<0>();
       }
+      GV1_MARK(5 + 2 * j);
       compute(gv_sb, t + stride);
+      GV1_MARK(6 + 2 * j);
     }
     // no LDS DMA may still be landing when the workgroup's LDS is handed on
     // (a wave without tasks still loaded one into its first slice)
@@ -1019,8 +1037,7 @@ __device__ __forceinline__ void gemv1k_body(const Gv1Args& a) {
       else if constexpr (FMT == CQ_Q5_K) part = gv3_superblock_q5k((const u4v*)sbp, xregs);
       else part = gv3_unit_legacy<FMT>(sbp, xregs);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) part += __shfl_xor(part, o, 64);
+    part = lane_group_sum(part, 64);
     if (lane == 0) gk_red[i & 1][wave] = part;
     __syncthreads();
     if (p == 0 && lane == 0 && r < a.N) {

@@ -261,15 +261,12 @@ __device__ __forceinline__ void gemv2_body(const Gv2Args& a) {
     if (ok) acc += gv2_quarter<FMT>(fb, p, u * GV1_XSTRIDE, 8 * u);
     if (a.R > 1) {
       // R rows of `units` superblocks: reduce within each group of 4 units lanes
-      float v = acc;
-      for (int o = 2 * a.units; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+      const float v = lane_group_sum(acc, 4 * a.units);
       finish(v, row, ok && (lane & (4 * a.units - 1)) == 0);
       acc = 0.0f;
     } else if (16 * (st - (int)(((uint32_t)st * (uint32_t)a.cinv) >> 16) * a.C) + 16 >= a.units) {
       // last step of this row: reduce the whole wave
-      float v = acc;
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+      const float v = lane_group_sum(acc, 64);
       finish(v, row, lane == 0);
       acc = 0.0f;
     }

@@ -50,11 +50,7 @@ __device__ __forceinline__ float gvr_reduce4(const float (&v)[GVR_RB], int lane)
     t2[k] = keep + __shfl_xor(send, 32, 64);
   }
   float t = (b4 ? t2[1] : t2[0]) + __shfl_xor(b4 ? t2[0] : t2[1], 16, 64);
-  t += __shfl_xor(t, 8, 64);
-  t += __shfl_xor(t, 4, 64);
-  t += __shfl_xor(t, 2, 64);
-  t += __shfl_xor(t, 1, 64);
-  return t;
+  return lane_group_sum(t, 16);
 }
 __device__ __forceinline__ int gvr_row_of_lane(int lane) { return ((lane >> 5) & 1) * 2 + ((lane >> 4) & 1); }
 

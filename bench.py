@@ -13,6 +13,14 @@ The K timed steps are captured once into a HIP graph (torch.cuda.CUDAGraph
 over the library's hipModuleLaunchKernel calls) and replayed, so the number
 measures the kernels back to back rather than Python's launch overhead.
 
+Sustained-load warm-up: the GPU's clocks settle only after tens of ms of
+continuous work (measured with back-to-back launches: Q6_K lm_head 94 us per
+launch in the first 4 ms, 72 us from ~25 ms on; Q4_K [14336 x 4096] 9.2 ->
+8.7 us), which is the state of a serving loop.  So before each timed
+section the same workload runs untimed for --warmup-ms (headline, default
+100 ms) or SECTION_WARM_MS (every other section), ending on buffers just
+before the timed ones.
+
 value = algorithmic bytes (GGUF-native weight bytes + x + y) of K steps
         / device time of the K steps (HIP events around one graph replay).
 The same graph is replayed until at least 100 launches have been timed, and
@@ -40,6 +48,18 @@ HBM_PEAK_GBS = 8000.0
 HEADLINE_KERNEL = "cq_gemv1_q4_k_yf32"  # what cq_matmul launches for m = 1, fp16 x, Q4_K [14336 x 4096]
 FP16_PEAK_TFLOPS = 2500.0
 MIN_LAUNCHES = 100
+SECTION_WARM_MS = 30.0
+
+
+def sustain(fn, ms):
+    """Run fn() (which enqueues device work) repeatedly, untimed, until ms
+    milliseconds of wall time have passed, synchronising every few calls."""
+    import torch
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(4):
+            fn()
+        torch.cuda.synchronize()
 
 
 def algo_bytes(wbytes, m, k, n, xbytes=2, ybytes=4):
@@ -114,6 +134,7 @@ def graph_time_us(launch, count, reps=None):
     launches, enough replays for >= MIN_LAUNCHES timed launches (at least 5);
     returns (median, stats)."""
     g = capture(launch, count)
+    sustain(g.replay, SECTION_WARM_MS)
     reps = reps or max(5, -(-MIN_LAUNCHES // count))
     st = stats(replay_times(g, count, reps))
     return st["median"], st
@@ -126,6 +147,11 @@ def eager_time_us(launch, count, reps=None):
     import torch
     launch(0)
     torch.cuda.synchronize()
+
+    def burst():
+        for i in range(count):
+            launch(i)
+    sustain(burst, SECTION_WARM_MS)
     reps = reps or max(5, -(-MIN_LAUNCHES // count))
     out = []
     for _ in range(reps):
@@ -316,6 +342,7 @@ def llama3_token(dev, ms=(1, 16)):
                 bufs["down"][l].matmul_into(x14, ys["down"])
             head.matmul_into(x4, yh)
         g = capture(token, 1)
+        sustain(g.replay, SECTION_WARM_MS)
         st = stats(replay_times(g, 1, 10))
         us = st["median"]
         out[f"m{m}"] = {"us_per_token_step": us, "tokens_per_s": round(m * 1e6 / us, 1),
@@ -477,6 +504,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--warmup-ms", type=float, default=100.0,
+                    help="untimed sustained load before the headline's timed replay (clock ramp)")
     ap.add_argument("--pool-gib", type=float, default=1.25)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
@@ -514,17 +543,23 @@ def main():
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-    # The K timed steps, captured once (starting on buffers the warmup did not
-    # touch) and replayed; the first replay is the timed region.
     K, W = args.steps, args.warmup
+    # The K timed steps, captured once (capture() also replays them once) and
+    # replayed; the first replay after the sustained load is the timed region.
     t_cap = time.perf_counter()
     g = capture(lambda i: step(W + i), K)
-    torch.cuda.synchronize()
+    # Sustained load: every pool buffer once per replay, ending on the step
+    # before W (so the timed steps start on buffers it did not touch last),
+    # replayed for --warmup-ms, then the timed replay with no gap.
+    gw = capture(lambda i: step(W - P + i), P)
+    sustain(gw.replay, args.warmup_ms)
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    gw.replay()
     a.record()
     g.replay()
     b.record()
     torch.cuda.synchronize()
+    del gw
     ms_total = a.elapsed_time(b)
     wall = time.perf_counter() - t_cap
     step_bytes = sum(algo_bytes(sz, 1, k, n) for sz, (n, k) in zip(sizes, shapes))
@@ -561,7 +596,7 @@ def main():
 
     line = {
         "metric": "Q4_K decode GEMV HBM GB/s (% of peak); prefill dequant-GEMM TFLOP/s",
-        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": K, "warmup": W, "warmup_ms": args.warmup_ms,
         "ms_per_step": round(ms_total / K, 5), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "q4_k", "data": "synthetic",
         "config": {"workload": "Q4_K decode GEMV, Llama-3-8B shapes [14336x4096]+[4096x14336], batch 1, x f16, "

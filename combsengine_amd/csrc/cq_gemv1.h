@@ -548,10 +548,16 @@ __device__ __forceinline__ float gv3_superblock_q6k(const uint8_t* sb, const Gv3
 #pragma unroll
           for (int jj = 0; jj < 4; jj++) {  // l = 16 g + 4 jj .. +3
             const uint32_t qlw = u4_word(ql4[g], jj), qhw = u4_word(qh4[g], jj);
-            const uint32_t q = ((qlw >> (4 * tt)) & 0x0F0F0F0Fu) | (((qhw >> (2 * t)) & 0x03030303u) << 4);
+            // per byte: bits 0-3 the ql nibble, 4-5 quadrant t's two qh
+            // bits (shifted there; bits 6-7 are left over from other
+            // fields), one bit-field insert; the 0x3F masks below drop 6-7
+            const uint32_t nl = tt ? qlw >> 4 : qlw;
+            const uint32_t hb = t == 0 ? qhw << 4 : t == 1 ? qhw << 2 : t == 2 ? qhw : qhw >> 2;
+            uint32_t q;  // (opaque to the compiler, which otherwise re-derives the fields with more operations)
+            asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(q) : "v"(0x0F0F0F0Fu), "v"(nl), "v"(hb));
             const int m = 32 * hh + 8 * t + 4 * g + jj;
-            s0 = fdot2u(q & 0x00FF00FFu, xr.xe[2 * m], s0);
-            s1 = fdot2u((q >> 8) & 0x00FF00FFu, xr.xe[2 * m + 1], s1);
+            s0 = fdot2u(q & 0x003F003Fu, xr.xe[2 * m], s0);
+            s1 = fdot2u((q >> 8) & 0x003F003Fu, xr.xe[2 * m + 1], s1);
           }
           const int si = 8 * hh + g + 2 * t;
           const float scf = (float)(int8_t)(scw[si >> 2] >> (8 * (si & 3)));

@@ -167,12 +167,20 @@ struct Gv1XStage {
 
 // The 8 scales and mins of a K-quant superblock header as floats.
 __device__ __forceinline__ void gv1_scales(const u4v& hd, float sc[8], float mn[8]) {
+  // All eight 6-bit scales (mins) as the four bytes of two words: sub-blocks
+  // 0-3 are the low six bits of bytes 0-3 of hd.y (hd.z); 4-7 take the low
+  // (high) nibble of hd.w's byte and, above it, the top two bits of hd.y's
+  // (hd.z's) byte (get_scale_min_k4), one bit-field insert per word.
+  uint32_t s47, m47;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(s47) : "v"(0x0F0F0F0Fu), "v"(hd.w), "v"(hd.y >> 2));
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(m47) : "v"(0x0F0F0F0Fu), "v"(hd.w >> 4), "v"(hd.z >> 2));
+  const uint32_t w[4] = {hd.y & 0x3F3F3F3Fu, hd.z & 0x3F3F3F3Fu, s47 & 0x3F3F3F3Fu, m47 & 0x3F3F3F3Fu};
 #pragma unroll
-  for (int j = 0; j < 8; j++) {
-    uint32_t s, m;
-    scale_min_k4(j, hd.y, hd.z, hd.w, s, m);
-    sc[j] = (float)s;
-    mn[j] = (float)m;
+  for (int j = 0; j < 4; j++) {
+    sc[j] = (float)((w[0] >> (8 * j)) & 0xFFu);
+    mn[j] = (float)((w[1] >> (8 * j)) & 0xFFu);
+    sc[4 + j] = (float)((w[2] >> (8 * j)) & 0xFFu);
+    mn[4 + j] = (float)((w[3] >> (8 * j)) & 0xFFu);
   }
 }
 
@@ -649,7 +657,7 @@ __device__ __forceinline__ float gv3_unit_legacy(const uint8_t* up, const Gv3XRe
         const uint32_t w = u4_word(q[i >> 2], i & 3) ^ 0x80808080u;
         const int m = 8 * blk + i;
         s0 = fdot2u(w & 0x00FF00FFu, xr.xe[2 * m], s0);
-        s1 = fdot2u((w >> 8) & 0x00FF00FFu, xr.xe[2 * m + 1], s1);
+        s1 = fdot2u(perm(w, w, 0x0C030C01u), xr.xe[2 * m + 1], s1);  // bytes 1, 3 to the low bytes of the halves
       }
       const float d = f16_bits_to_f32(ld_u16(bp));
       acc = __builtin_fmaf(d, __builtin_fmaf(16777216.0f, s0 + s1, -128.0f * xr.su[blk]), acc);

@@ -820,15 +820,34 @@ static cq_status launch_gemv1k(DeviceModule* dm, const cq_weight* w, const void*
 // not fill whole waves, where cq_gemv1 leaves lanes idle: Qwen2.5-7B 3584 x 3584 5.75 against 6.05 us, 18944 x 3584 11.9
 // against 13.7, 3584 x 18944 13.9 against 14.5 (cq_gemv1k); on the
 // Llama-3-8B shapes (16 and 56 units) cq_gemv1 measured faster (9.7 against
-// 10.2 us at 14336 x 4096, 10.4 against 10.6 at 4096 x 14336).  So it is the
-// default below 16 units and above 64 (where cq_gemv1k would run).
-// COMBS_GEMVR=0 never, 2 always where it fits.
+// 10.2 us at 14336 x 4096, 10.4 against 10.6 at 4096 x 14336), and so it did
+// on power-of-two rows below 16 units (graph-replayed, sustained load:
+// 16384 x 2048 7.17 against 7.90 us) and on short rows (8960 x 1536, 6
+// units: 6.01 against 7.49).  So it is the default on rows of a
+// non-power-of-two count from 9 to 63 units and above 64 (where cq_gemv1k
+// would run); small Q4_K weights take the quarter-superblock kernel cq_gemv2
+// first (see q4k_small_gemv2).  COMBS_GEMVR=0 never, 2 always where it
+// fits.
 constexpr int kGvrMaxK = 32768;
 constexpr int kGvrWaves = 8;
 static bool gemvr_fits(const cq_weight* w) {
   return w->format == CQ_Q4_K && w->k % 256 == 0 && w->k <= kGvrMaxK;
 }
-static bool gemvr_default(const cq_weight* w) { return w->k / 256 < 16 || w->k / 256 > 64; }
+static bool gemvr_default(const cq_weight* w) {
+  const int64_t u = w->k / 256;
+  return u > 64 || (u >= 9 && u < 64 && (u & (u - 1)) != 0);
+}
+// Q4_K weights of fewer than 65536 superblocks (m = 1): the quarter-
+// superblock streaming kernel cq_gemv2 is the fastest of the three
+// (graph-replayed, sustained load, us: 1024 x 3584 4.12 against 4.87 for
+// cq_gemv1 and 5.26 for cq_gemvr; 4096 x 3584 5.29 / 5.69 / 5.78; 2048 x
+// 2048 4.14 / 4.34 / 5.25; 1024 x 4096 4.09 / 4.50 / 5.23; 896 x 1536 3.91 /
+// 5.33 / 5.13); not at 65536 (8192 x 2048, 4096 x 4096) and above, nor on
+// short rows from 32768 (8960 x 1536: 7.75 against 6.01 for cq_gemv1).
+static bool q4k_small_gemv2(const cq_weight* w) {
+  const int64_t u = w->k / 256, sb = w->n * u;
+  return w->format == CQ_Q4_K && (sb < 32768 || (sb < 65536 && u >= 14));
+}
 static cq_status launch_gemvr(DeviceModule* dm, const cq_weight* w, const void* x, void* y, int yt, hipStream_t s,
                               const CqEpi& epi) {
   GvrArgs a{};
@@ -1150,10 +1169,12 @@ static cq_status matmul_impl(const cq_weight* w, const void* x, int x_dtype, int
     return launch_gemml(dm, w, x, m, y, yt, (hipStream_t)stream, epi);
   if (m == 1 && !xt && path != CQ_PATH_GEMV && knobs().gemv1) {
     // quarter-superblock streaming kernel (cq_gemv2): COMBS_GEMV2=2 for
-    // every K-quant, =1 for Q6_K, 0 (default) only where cq_gemv1 does not
-    // fit (a K-quant weight whose bytes are not 16-byte aligned)
+    // every K-quant, =1 for Q6_K, 0 (default) for small Q4_K weights
+    // (q4k_small_gemv2) and where cq_gemv1 does not fit (a K-quant weight
+    // whose bytes are not 16-byte aligned), -1 only there
     const int g2 = knobs().gemv2;
-    if (kq && (g2 == 2 || (g2 == 1 && w->format == CQ_Q6_K)) && gemv2_fits(w))
+    if (kq && (g2 == 2 || (g2 == 1 && w->format == CQ_Q6_K) || (g2 == 0 && !epi.bias && !epi.aux && q4k_small_gemv2(w))) &&
+        gemv2_fits(w))
       return launch_gemv2(dm, w, x, y, yt, (hipStream_t)stream, epi);
     if (gemvr_fits(w) && !epi.bias && !epi.aux && (knobs().gemvr == 2 || (knobs().gemvr == 1 && gemvr_default(w))))
       return launch_gemvr(dm, w, x, y, yt, (hipStream_t)stream, epi);

@@ -174,7 +174,8 @@ def test_gemv_single_row(cuda, monkeypatch, fmt, n, k, kernel):
     forces the fp16-register path, gemv1i8 the int8 path for Q4_K / Q4_0 /
     Q8_0; small weights spread their tasks wave-major over the grid,
     gemv1packed packs them workgroup-major) and the 16-row MFMA kernel; fp32
-    and fp16 outputs."""
+    and fp16 outputs.  (COMBS_GEMV2=-1 keeps the small Q4_K weights, which
+    take gemv2 by default, on the kernel named.)"""
     import torch
     if kernel == "gemv2" and fmt in LEGACY:
         pytest.skip("gemv2 serves the K-quants")
@@ -182,7 +183,7 @@ def test_gemv_single_row(cuda, monkeypatch, fmt, n, k, kernel):
         pytest.skip("the row-split kernel serves Q4_K")
     monkeypatch.setenv("COMBS_GEMVR", "2" if kernel == "gemvr" else "0")
     monkeypatch.setenv("COMBS_GEMV1", "0" if kernel == "mfma" else "1")
-    monkeypatch.setenv("COMBS_GEMV2", "2" if kernel == "gemv2" else "0")
+    monkeypatch.setenv("COMBS_GEMV2", "2" if kernel == "gemv2" else "-1")
     monkeypatch.setenv("COMBS_GEMV1_I8", {"gemv1reg": "0", "gemv1i8": "2"}.get(kernel, "1"))
     monkeypatch.setenv("COMBS_GEMV1_SPREAD", "0" if kernel == "gemv1packed" else "1")
     data = synth(fmt, n, k)

@@ -62,6 +62,7 @@ def test_gemv1_many_tasks_per_wave(cuda, monkeypatch, fmt, n, k):
     # fp16-register kernels where they serve the format
     monkeypatch.setenv("COMBS_GEMV1_I8", "0")
     monkeypatch.setenv("COMBS_GEMVR", "0")  # cq_gemv1 on every grid
+    monkeypatch.setenv("COMBS_GEMV2", "-1")
     for grid in ("1", "2", "3", "default"):
         if grid == "default":
             monkeypatch.delenv("COMBS_GEMV1_GRID", raising=False)

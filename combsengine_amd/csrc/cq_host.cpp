@@ -823,10 +823,10 @@ static cq_status launch_gemv1k(DeviceModule* dm, const cq_weight* w, const void*
 // 10.2 us at 14336 x 4096, 10.4 against 10.6 at 4096 x 14336), and so it did
 // on power-of-two rows below 16 units (graph-replayed, sustained load:
 // 16384 x 2048 7.17 against 7.90 us) and on short rows (8960 x 1536, 6
-// units: 6.01 against 7.49).  So it is the default on rows of a
-// non-power-of-two count from 9 to 63 units and above 64 (where cq_gemv1k
-// would run); small Q4_K weights take the quarter-superblock kernel cq_gemv2
-// first (see q4k_small_gemv2).  COMBS_GEMVR=0 never, 2 always where it
+// units: 6.01 against 7.49).  So it is the default on rows of 9 to 15
+// units (Qwen2.5's 3584: 8192 x 3584 6.56 against 7.45) and above 64 (where
+// cq_gemv1k would run); small Q4_K weights take the quarter-superblock
+// kernel cq_gemv2 first (see q4k_small_gemv2).  COMBS_GEMVR=0 never, 2 always where it
 // fits.
 constexpr int kGvrMaxK = 32768;
 constexpr int kGvrWaves = 8;
@@ -835,7 +835,7 @@ static bool gemvr_fits(const cq_weight* w) {
 }
 static bool gemvr_default(const cq_weight* w) {
   const int64_t u = w->k / 256;
-  return u > 64 || (u >= 9 && u < 64 && (u & (u - 1)) != 0);
+  return u > 64 || (u >= 9 && u < 16);
 }
 // Q4_K weights of fewer than 65536 superblocks (m = 1): the quarter-
 // superblock streaming kernel cq_gemv2 is the fastest of the three

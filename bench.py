@@ -351,9 +351,9 @@ def llama3_token(dev, ms=(1, 16)):
 
 
 def secondary(dev):
-    """Prefill dequant-GEMM (config 4), eager (through fast_launcher: the
-    library may split K) and captured as a graph (no K split under capture)
-    reported separately; lm_head Q6_K; the gated gate/up; batch 4/16."""
+    """Prefill dequant-GEMM (config 4), eager (through fast_launcher) and
+    captured as a graph (both may split K) reported separately; lm_head Q6_K;
+    the gated gate/up; batch 4/16."""
     import numpy as np
     import torch
     from combsengine_amd import QuantFormat

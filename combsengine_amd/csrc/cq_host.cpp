@@ -1029,12 +1029,22 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
   // superblocks: at N = 512, K = 3584, m = 512 four slices of 3-4 measured
   // 27 / 23 us (Q4_K / Q6_K) against 31 / 32 us for two; slices of 2 were
   // slower at N = 1024, K = 4096); COMBS_GEMM2_SPLIT forces the slice count.
-  // Not while the stream is being captured into a graph: split-K inside a
-  // captured graph has not been verified on the GPU, so captured launches
-  // take the unsplit path.
+  // While the stream is being captured into a graph the scratch (sums and
+  // partials) comes from the device's fixed buffer (as for
+  // cq_matmul_noalloc), so the graph holds kernel nodes only, no
+  // allocations; captured launches then share that buffer with each other
+  // and with cq_matmul_noalloc calls (replays that overlap on one device
+  // race).  If its address cannot be had, a captured launch takes no split
+  // and allocates its sums stream-ordered.
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   if (!g_plan) HIP_TRY(hipStreamIsCapturing(s, &cs));
-  int splits = cs == hipStreamCaptureStatusNone ? knobs().gemm2_split : 1;
+  const FixedScratch* fixed = g_fixed;
+  FixedScratch cap_fs{nullptr, 0};
+  if (!fixed && cs != hipStreamCaptureStatusNone) {
+    if (cq_scratch_device_ptr(&cap_fs.ptr, &cap_fs.bytes) == hipSuccess) fixed = &cap_fs;
+    else (void)hipGetLastError();
+  }
+  int splits = (cs == hipStreamCaptureStatusNone || fixed) ? knobs().gemm2_split : 1;
   if (splits < 1) {
     splits = 1;
     while (gx * mblk * splits * 2 <= slots && a.units / (splits * 2) >= 3) splits *= 2;
@@ -1049,18 +1059,21 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
     const int n_sp = (a.units + us - 1) / us;
     return n_sp > 1 ? (size_t)n_sp * m * w->n * 4 : 0;
   };
-  if (g_fixed) {
-    if (sums_bytes > g_fixed->bytes)
+  if (fixed && sums_bytes > fixed->bytes) {
+    if (g_fixed)
       return fail(CQ_ERR_BAD_SHAPE,
                   "no-alloc prefill: activation sums of %lld x %lld need %zu bytes, the fixed scratch holds %zu",
                   (long long)m, (long long)w->k, sums_bytes, g_fixed->bytes);
-    while (splits > 1 && sums_bytes + part_size(splits) > g_fixed->bytes) splits /= 2;
+    fixed = nullptr;  // captured, sums too large for the fixed buffer: no split, sums allocated
+    splits = 1;
   }
+  if (fixed)
+    while (splits > 1 && sums_bytes + part_size(splits) > fixed->bytes) splits /= 2;
   a.usplit = (a.units + splits - 1) / splits;
   splits = (a.units + a.usplit - 1) / a.usplit;
   const size_t part_bytes = splits > 1 ? (size_t)splits * m * w->n * 4 : 0;
   void* ws = nullptr;
-  if (g_fixed) ws = g_fixed->ptr;
+  if (fixed) ws = fixed->ptr;
   else if ((sums_bytes + part_bytes) && !g_plan) HIP_TRY(hipMallocAsync(&ws, sums_bytes + part_bytes, s));
   auto launch_all = [&]() -> hipError_t {
     hipError_t e;
@@ -1084,7 +1097,7 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
     return klaunch(dm, dm->reduce[yt], (unsigned)((mn + 255) / 256), 1, 1, 256, 0, s, rp);
   };
   const hipError_t e = launch_all();
-  if (ws && !g_fixed) HIP_TRY(hipFreeAsync(ws, s));
+  if (ws && !fixed) HIP_TRY(hipFreeAsync(ws, s));
   if (e != hipSuccess) return fail(CQ_ERR_HIP, "prefill GEMM launch: %s", hipGetErrorString(e));
   return CQ_OK;
 }

@@ -103,7 +103,11 @@ const void* cq_weight_device_ptr(const cq_weight* w);
  * QuantLinearOp::forward it serves (qlinear.rs:58).  x: device, x_dtype
  * CQ_F16 or CQ_F32; y: device, caller-allocated, y_dtype CQ_F32 or CQ_F16.
  * fp32 activations must be finite and below 65504 in magnitude (they are fed
- * to the fp16 matrix cores as a hi+lo pair). */
+ * to the fp16 matrix cores as a hi+lo pair).  Prefill (m > 16) takes
+ * stream-ordered scratch; while the stream is being captured into a HIP
+ * graph it takes the device's fixed array instead (see cq_matmul_noalloc),
+ * which graphs captured this way share: replays that overlap on one device
+ * race. */
 cq_status cq_matmul(const cq_weight* w, const void* x, int x_dtype, int64_t m, void* y, int y_dtype,
                     void* stream);
 

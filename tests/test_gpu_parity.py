@@ -307,8 +307,8 @@ def test_gemm_gaussian_prefill_shape(cuda, fmt):
 def test_graph_capture_replays(cuda, monkeypatch):
     """cq_matmul launches captured into a HIP graph replay correctly, with
     eager work and synchronisations between replays (no memset nodes: the
-    library records none).  Captured prefill launches take no K split, so
-    the eager reference is pinned to the unsplit path for bit equality.
+    library records none).  The K split is pinned to one slice here (the
+    captured split is test_graph_capture_prefill_split's).
     The graph holds single-row decode of a small weight (tasks spread over
     the grid), batched decode (m = 8), prefill (m = 64) and single-row
     decode of a 74-superblock Q6_K row (the row-half kernel)."""
@@ -349,6 +349,50 @@ def test_graph_capture_replays(cuda, monkeypatch):
         torch.cuda.synchronize()
         for i, (_, _, y) in enumerate(cases):
             assert torch.equal(y, refs[i]), (rep, i)
+
+
+@pytest.mark.parametrize("fmt,n,k,m", [(QuantFormat.Q6K, 512, 3584, 512), (QuantFormat.Q4K, 512, 3584, 130),
+                                        (QuantFormat.Q5K, 300, 4096, 40), (QuantFormat.Q4K, 1024, 4096, 256)])
+def test_graph_capture_prefill_split(cuda, fmt, n, k, m):
+    """Prefill captured into a HIP graph with the default K split: the
+    captured launch takes its activation sums and split partials from the
+    device's fixed scratch buffer (no allocation in the graph) and must give
+    the eager launch's bits (same kernels and slices, eager scratch allocated
+    stream-ordered) on every replay, with eager prefill and a no-allocation
+    call (which overwrites the fixed buffer) between the replays."""
+    import torch
+    rng = np.random.default_rng(40 + int(fmt) + m)
+    data = quantize(fmt, rng.normal(0, 0.02, (n, k)).astype(np.float32))
+    w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
+    wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
+    x = torch.from_numpy(rng.normal(0, 1, (m, k)).astype(np.float16)).cuda()
+    y = torch.empty((m, n), dtype=torch.float16, device="cuda")
+    kern = L.kernels(w, L.CQ_F16, m, L.CQ_F16)
+    print(f"captured prefill {fmt.name} [{n}x{k}] m={m} kernels={kern}", flush=True)
+    assert "splitk" in kern, "the shape is meant to take a K split"
+    w.matmul_into(x, y)
+    torch.cuda.synchronize()
+    ref = y.clone()
+    O.assert_close(ref.float().cpu().numpy(), x.double().cpu().numpy() @ wd.astype(np.float64).T, 1e-3, "eager")
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            w.matmul_into(x, y)
+    torch.cuda.current_stream().wait_stream(s)
+    x2 = torch.from_numpy(rng.normal(0, 1, (m // 2 + 1, k)).astype(np.float16)).cuda()
+    y2 = torch.empty((x2.shape[0], n), dtype=torch.float16, device="cuda")
+    for rep in range(4):
+        y.fill_(float("nan"))
+        w.matmul_into(x2, y2)  # eager prefill between replays
+        st = L.lib().cq_matmul_noalloc(w.handle, x2.data_ptr(), L.CQ_F16, x2.shape[0], y2.data_ptr(), L.CQ_F16,
+                                       torch.cuda.current_stream().cuda_stream)
+        assert st == L.CQ_OK, L.last_error()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref), rep
 
 
 @pytest.mark.parametrize("fmt", KQ)

@@ -1,0 +1,207 @@
+// Decode GEMV for a few fp16 activation rows (2 <= m <= 16), K-quant
+// weights of at most 16 superblocks per row (K <= 4096), with every
+// activation fragment loaded once per workgroup (cq_gemvq_*):
+// y[m, n] = sum_k x[m, k] * W[n, k].
+// Replaces qmatmul.rs:881-930 (Q4_K), :1064-1117 (Q5_K) and :1184-1229
+// (Q6_K) for batched decode.
+//
+// Why.  In the MFMA operand layout a lane holds 8 consecutive activations of
+// one row, so a 16-byte-per-lane load of A fragments touches 16 rows x 4
+// k-groups = 64 distinct 128-byte lines per instruction; reading the m x K
+// activation block that way once per 16-row tile (cq_gemvd) is bound by
+// cache-line traffic, not bytes (measured: the activation loads alone of a
+// 14336 x 4096 weight at m = 16 take 7 us).  And a tile's weight bytes,
+// fetched as 16-byte pieces of 16 rows at a row stride, stream poorly.
+//
+// Work mapping.
+//   - Wave u of a workgroup owns superblock column u (the workgroup has one
+//     wave per superblock of a row).  Its activations (m rows x 256 values)
+//     arrive once, by LDS DMA (global_load_lds, whole 512-byte row pieces,
+//     two rows per instruction) through its ring, and are read into
+//     registers in the operand layout (8 x 16 bytes per lane), where they
+//     stay for the whole launch.
+//   - The workgroup walks a contiguous range of 16-row tiles (the grid is
+//     at most one workgroup per compute unit, the tiles split as evenly as
+//     floor division allows).  Each wave streams its column of every tile
+//     (16 rows x one superblock, each row's bytes from the 16-byte boundary
+//     at or below the superblock) through a ring of R slots of its own by
+//     LDS DMA, waiting for a slot by position in the in-order load counter,
+//     so no wave waits for another while loading.  Dynamic LDS per wave:
+//     the ring (R x NI KB), then 1 KB of the workgroup's partial sums.
+//   - Each wave keeps its 16 x 16 partial blocks (4 fp32 per lane) of
+//     TC tiles (as many as LDS allows: 1 to 4) in registers; then they
+//     are added across the waves in LDS in wave order, one thread per
+//     output (one barrier pair per chunk), and stored through the epilogue.
+//     (Reducing after every tile made every wave wait for the slowest
+//     wave's weight bytes once per tile: 13.2 against 10.3 us with no
+//     reduction at all, Q4_K 14336 x 4096 at m = 2.)
+//   - Superblock arithmetic is the MFMA GEMV's (cq_gemv.h: exact q * sc
+//     fp16 operands, d / dmin on the fp32 results, the K-quant min term as
+//     an MFMA against the 6-bit mins).
+// Activation rows >= m are read as row m - 1 (their outputs are not
+// stored); weight rows >= n are read as row n - 1 (likewise).
+#pragma once
+#include "cq_gemvd.h"
+#include "cq_gemv1.h"
+
+#define GVQ_MAX_WAVES 16
+
+struct GvqArgs {
+  const uint8_t* w;   // packed superblocks, [N rows][row_bytes]
+  const _Float16* x;  // [M][K]
+  void* y;            // [M][N] fp32 or fp16
+  long long row_bytes;
+  long long wbytes;   // weight bytes (the DMA never reads past them)
+  int M, N, K, units;  // units = K / 256 = waves per workgroup
+  int tiles;           // ceil(N / 16)
+  CqEpi epi;
+};
+
+// 16-byte pieces of one row's superblock in a slot and DMA instructions per
+// slot (64 pieces each); two slots per wave.
+template <int FMT>
+struct GvqShape {
+  static constexpr int BB = FmtTraits<FMT>::bytes;
+  static constexpr int PR = BB % 16 == 0 ? BB / 16 : (BB + 15) / 16 + 1;
+  static constexpr int NI = (16 * PR + 63) / 64;
+  static constexpr int R = 2;
+  // tiles per cross-wave reduction: their partial sums live in registers
+  // and then 1 KB per wave and tile of LDS, whatever of a wave's 10 KB
+  // share of the 160 KB the ring leaves
+  static constexpr int TC = 10 - R * NI;
+  static constexpr int WAVE_PIECES = 10 * 64;  // u4v per wave: ring, then partial sums
+};
+
+template <int FMT, int YT>
+__device__ __forceinline__ void gemvq_body(const GvqArgs& a) {
+  typedef GvqShape<FMT> S;
+  constexpr int BB = S::BB, PR = S::PR, NI = S::NI, R = S::R, TC = S::TC;
+  extern __shared__ __attribute__((aligned(16))) u4v gq_lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = a.units;
+  const int j = lane & 15, g = lane >> 4;
+  u4v* ring = gq_lds + wave * S::WAVE_PIECES;
+  // partial sums of wave w, tile tt of a chunk: TC KB after w's ring
+  auto red_at = [&](int w, int tt, int r, int ln) -> float& {
+    return ((float*)(gq_lds + w * S::WAVE_PIECES + R * NI * 64))[(tt * 4 + r) * 64 + ln];
+  };
+  const uint32_t rb = gv3_lds_addr(ring);
+  // this workgroup's tiles [t0, t0 + nmine)
+  const int G = (int)gridDim.x;
+  const int t0 = (int)((long long)blockIdx.x * a.tiles / G);
+  const int nmine = (int)((long long)(blockIdx.x + 1) * a.tiles / G) - t0;
+
+  // Weight pieces of this lane: piece q = 64 i + lane of a slot is piece
+  // q % PR of row q / PR's superblock (from its 16-byte boundary).
+  int prow[NI], poff[NI];
+#pragma unroll
+  for (int i = 0; i < NI; i++) {
+    const int q = min(64 * i + lane, 16 * PR - 1);
+    prow[i] = q / PR;
+    poff[i] = 16 * (q - prow[i] * PR);
+  }
+  const size_t col = (size_t)wave * BB;
+  const size_t wlast = (size_t)a.wbytes - 16;
+  auto dma = [&](int t) {  // tile t0 + t into slot t % R
+    const int n0 = 16 * (t0 + t);
+    const uint32_t lb = rb + 1024 * NI * (t % R);
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      const size_t s = (size_t)min(n0 + prow[i], a.N - 1) * (size_t)a.row_bytes + col;
+      gv3_dma16(a.w + min((s & ~(size_t)15) + poff[i], wlast), lb + 1024 * i);
+    }
+  };
+  // the lane's row within a slot: byte offset of its superblock
+  auto my_off = [&](int t) {
+    const size_t s = (size_t)min(16 * (t0 + t) + j, a.N - 1) * (size_t)a.row_bytes + col;
+    return (int)(s & 15);
+  };
+  // Activations of column `wave`, carried by the wave's LDS after slot 0
+  // (slot 1 and the partial sums' space) in phases of PH row pairs while
+  // tile 0's weights land in slot 0 (their HBM latency hides the first
+  // phase's; one phase up to 14 rows, 12 for Q6_K): DMA instruction p brings rows 2p
+  // (even lanes) and 2p + 1 (odd lanes), piece (lane >> 1) ^ p of each
+  // row's 32 16-byte pieces, so that the 16 rows' reads of one fragment
+  // fall on 16 distinct 16-byte bank groups.
+  constexpr int PH = 10 - NI;
+  dma(0);
+  const int pairs = (a.M + 1) >> 1;
+  const int xr = min(j, a.M - 1), xp = xr >> 1;  // the lane's activation row and its pair
+  h8 xa[8] = {};
+  for (int p0 = 0; p0 < pairs; p0 += PH) {
+    const int pe = min(p0 + PH, pairs);
+    for (int p = p0; p < pe; p++) {
+      const int r = min(2 * p + (lane & 1), a.M - 1);
+      gv3_dma16(a.x + (size_t)r * a.K + 256 * wave + 8 * ((lane >> 1) ^ p), rb + 1024 * (NI + p - p0));
+    }
+    gv3_wait_vm<0>();
+    if (xp >= p0 && xp < pe) {
+      const uint8_t* base = (const uint8_t*)ring + 1024 * (NI + xp - p0) + 16 * (xr & 1);
+#pragma unroll
+      for (int s = 0; s < 8; s++) {
+        const int piece = (gvd_abase<FMT>(g) + gvd_aoff<FMT>(s)) >> 3;  // fragment s of lane group g
+        xa[s] = __builtin_bit_cast(h8, ld_u128(base + 32 * (piece ^ xp)));
+      }
+    }
+    // the slots are reused only after these reads have completed
+#pragma unroll
+    for (int s = 0; s < 8; s++) asm volatile("" ::"v"(xa[s]));
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    asm volatile("" ::: "memory");
+  }
+
+  for (int t = 1; t < R - 1 && t < nmine; t++) dma(t);
+  // Tiles in chunks of TC: each wave keeps its partial sums of a chunk
+  // in registers and the chunk is added across waves afterwards, so that
+  // within a chunk no wave waits for another.
+  for (int c0 = 0; c0 < nmine; c0 += TC) {
+    f4 acc[TC];
+#pragma unroll
+    for (int tt = 0; tt < TC; tt++) {
+      const int t = c0 + tt;
+      if (t < nmine) {
+        // refill the slot of tile t - 1 (read completely) with tile
+        // t + R - 1; near the end nothing is refilled and every load still
+        // in flight is waited for
+        if (t + R - 1 < nmine) {
+          dma(t + R - 1);
+          gv3_wait_vm<NI * (R - 1)>();  // tile t landed; tiles t + 1 .. t + R - 1 may be in flight
+        } else {
+          gv3_wait_vm<0>();
+        }
+        const uint8_t* wp = (const uint8_t*)ring + 1024 * NI * (t % R) + 16 * PR * j + my_off(t);
+        typename FmtTraits<FMT>::Frag f;
+        load_unit<FMT>(f, wp, g, 0);
+        acc[tt] = gvd_superblock<FMT>(f, xa, g);
+        // this slot is refilled in a later iteration: its reads must be done
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        asm volatile("" ::: "memory");
+      }
+    }
+    // the chunk's partial sums, [wave][tile][r][lane], added by one thread
+    // per output: all partials in flight at once, then summed in wave order
+#pragma unroll
+    for (int tt = 0; tt < TC; tt++)
+      if (c0 + tt < nmine)
+#pragma unroll
+        for (int r = 0; r < 4; r++) red_at(wave, tt, r, lane) = acc[tt][r];
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < 256 * TC; idx += blockDim.x) {
+      const int tt = idx >> 8, r = (idx >> 6) & 3, ln = idx & 63;
+      if (c0 + tt < nmine) {
+        float v[GVQ_MAX_WAVES];
+#pragma unroll
+        for (int w2 = 0; w2 < GVQ_MAX_WAVES; w2++) v[w2] = w2 < nw ? red_at(w2, tt, r, ln) : 0.0f;
+        float s = v[0];
+#pragma unroll
+        for (int w2 = 1; w2 < GVQ_MAX_WAVES; w2++)
+          if (w2 < nw) s += v[w2];
+        const int m = 4 * (ln >> 4) + r, n = 16 * (t0 + c0 + tt) + (ln & 15);
+        if (m < a.M && n < a.N) cq_store<YT>(a.y, a.epi, s, (size_t)m * a.N + n, n);
+      }
+    }
+    __syncthreads();  // partial sums read before the next chunk writes them
+  }
+  gv3_wait_vm<0>();  // no LDS DMA may still be landing when the workgroup ends
+}

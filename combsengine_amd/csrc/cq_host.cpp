@@ -6,6 +6,7 @@
 // launch geometry and error reporting: there is no host compute path.
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
@@ -143,6 +144,15 @@ struct LtArgs {
   int M, N, K, units, usplit;
   CqEpi epi;
 };
+struct GvqArgs {
+  const void* w;
+  const void* x;
+  void* y;
+  long long row_bytes;
+  long long wbytes;
+  int M, N, K, units, tiles;
+  CqEpi epi;
+};
 constexpr int kMultiMax = 4;  // weights per cq_matmul_multi launch (GV1_MSEG)
 struct Gv1Args {
   const void* w;
@@ -227,6 +237,7 @@ struct DeviceModule {
   hipFunction_t gemv2[kNumFormats][2][2] = {};  // K-quants only     // [format][y f16]
   hipFunction_t gemvd[kNumFormats][3][2] = {};  // K-quants only: [format][NT 1, 2, 4][y f16]
   hipFunction_t gemvs[kNumFormats][2] = {};  // K-quants only: [format][y f16]
+  hipFunction_t gemvq[kNumFormats][2] = {};  // K-quants only: [format][y f16]
   hipFunction_t gemml[kNumFormats][2][2] = {};  // 32-value formats only: [format][NT - 1][y f16]
   hipFunction_t gemvr[2][4] = {};  // Q4_K rows split across lanes: [y f16][log2 activation pieces per thread]
   int cus = 0;                        // compute units of the device
@@ -259,7 +270,7 @@ void load_module(DeviceModule& d, int dev) {
   // last-error state for the caller's next check to find.
   auto get = [&d](hipFunction_t* f, const char* nm) {
     const std::string n(nm);
-    const int mi = (n.rfind("cq_gemv1", 0) == 0 || n.rfind("cq_gemvr", 0) == 0) ? 1 : n.rfind("cq_gemv2", 0) == 0 ? 2
+    const int mi = (n.rfind("cq_gemv1", 0) == 0 || n.rfind("cq_gemvr", 0) == 0) ? 1 : (n.rfind("cq_gemv2", 0) == 0 || n.rfind("cq_gemvq", 0) == 0) ? 2
                    : (n.rfind("cq_gemm", 0) == 0 || n.rfind("cq_xsums", 0) == 0 || n.rfind("cq_splitk", 0) == 0) ? 3
                    : 0;
     const hipError_t e = hipModuleGetFunction(f, d.mods[mi], nm);
@@ -369,6 +380,11 @@ void load_module(DeviceModule& d, int dev) {
         d.err = std::string("missing kernel ") + name;
         return;
       }
+      snprintf(name, sizeof name, "cq_gemvq_%s_y%s", fmt_name(kFormats[fi]), yt ? "f16" : "f32");
+      if (get(&d.gemvq[fi][yt], name) != hipSuccess) {
+        d.err = std::string("missing kernel ") + name;
+        return;
+      }
     }
   }
   for (int yt = 0; yt < 2; yt++)
@@ -411,7 +427,8 @@ constexpr int kUnset = -1000000;
 struct Knobs {
   int gemv_waves, gemv1, gemv1k, gemv1_grid, gemv1_i8, gemv1_prefetch2, gemv1_span, gemv1_spread,
       gemv1_wave_major, gemv2, gemv2_wpc, gemvd, gvd_nt, gvd_waves, gemm_kernel, gemm_waves, gemm2_mt,
-      gemm2_nt, gemm2_split, gateup_fused, gemvr, gemvs, gemvs_split, gemml, gemml_nt, multi_fused;
+      gemm2_nt, gemm2_split, gateup_fused, gemvr, gemvs, gemvs_split, gemvq, gemvq_groups, gemml, gemml_nt,
+      multi_fused;
 };
 Knobs g_knobs;
 std::once_flag g_knobs_once;
@@ -445,6 +462,8 @@ void read_knobs() {
   k.gemvr = env_int("COMBS_GEMVR", 1);
   k.gemvs = env_int("COMBS_GEMVS", 1);
   k.gemvs_split = env_int("COMBS_GEMVS_SPLIT", 0);
+  k.gemvq = env_int("COMBS_GEMVQ", 1);
+  k.gemvq_groups = env_int("COMBS_GEMVQ_GROUPS", 0);
   k.gemml = env_int("COMBS_GEMML", 1);
   k.gemml_nt = env_int("COMBS_GEMML_NT", 0);
   k.multi_fused = env_int("COMBS_MULTI_FUSED", 1);
@@ -741,6 +760,45 @@ static cq_status launch_gemvs(DeviceModule* dm, const cq_weight* w, const void* 
   }
   if (ws && !g_fixed) HIP_TRY(hipFreeAsync(ws, s));
   if (e != hipSuccess) return fail(CQ_ERR_HIP, "batched decode launch: %s", hipGetErrorString(e));
+  return CQ_OK;
+}
+
+// Batched decode with every activation fragment loaded once per workgroup
+// (cq_gemvq_*, K-quants, 2 <= m <= 16, at most 16 superblocks per row):
+// one wave per superblock column, workgroups over balanced ranges of 16-row
+// tiles, at most as many workgroups as fit on the compute units at once.
+// LDS per wave: 10 KB, a DMA ring of two slots (3 KB for Q4_K / Q5_K, 4 KB
+// for Q6_K), which also carries the activation transit, and the rest for
+// the partial sums of 1 KB per tile of a reduction chunk.
+// Needs the weight, its size and the activations 16-byte aligned (whole
+// 16-byte DMA pieces).
+static bool gemvq_fits(const cq_weight* w, const void* x) {
+  return gemvs_fits(w) && w->k / 256 <= 16 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+}
+static int gemvq_lds_bytes(int nw) { return nw * 10 * 1024; }
+static cq_status launch_gemvq(DeviceModule* dm, const cq_weight* w, const void* x, int64_t m, void* y, int yt,
+                              hipStream_t s, const CqEpi& epi) {
+  const int fi = fmt_index(w->format);
+  GvqArgs a{};
+  a.w = w->dev;
+  a.x = x;
+  a.y = y;
+  a.row_bytes = (long long)(w->nbytes / (size_t)w->n);
+  a.wbytes = (long long)w->nbytes;
+  a.M = (int)m;
+  a.N = (int)w->n;
+  a.K = (int)w->k;
+  a.units = (int)(w->k / 256);
+  a.epi = epi;
+  const long long tiles = (w->n + 15) / 16;
+  if (tiles > 0x7fffffffLL) return fail(CQ_ERR_BAD_SHAPE, "grid too large (n=%lld)", (long long)w->n);
+  a.tiles = (int)tiles;
+  const int lds = gemvq_lds_bytes(a.units);
+  const int per_cu = std::max(1, std::min(160 * 1024 / lds, 16 / a.units));
+  long long groups = knobs().gemvq_groups > 0 ? knobs().gemvq_groups : (long long)dm->cus * per_cu;
+  groups = std::min(groups, tiles);
+  void* params[] = {&a};
+  HIP_TRY(klaunch(dm, dm->gemvq[fi][yt], (unsigned)groups, 1, 1, 64 * a.units, (unsigned)lds, s, params));
   return CQ_OK;
 }
 
@@ -1195,6 +1253,8 @@ static cq_status matmul_impl(const cq_weight* w, const void* x, int x_dtype, int
     if (gemv1k_fits(w) && knobs().gemv1k) return launch_gemv1k(dm, w, x, y, yt, (hipStream_t)stream, epi);
     if (kq && w->k / 256 <= 64 && gemv2_fits(w)) return launch_gemv2(dm, w, x, y, yt, (hipStream_t)stream, epi);
   }
+  if (kq && !xt && m >= 2 && m <= 16 && knobs().gemvq && gemvq_fits(w, x))
+    return launch_gemvq(dm, w, x, m, y, yt, (hipStream_t)stream, epi);
   if (kq && !xt && m >= 2 && m <= 16 && gemvs_fits(w)) {
     if (knobs().gemvs == 1 && w->n >= (int64_t)16 * kGvsWaves * dm->cus)
       return launch_gemvs(dm, w, x, m, y, yt, (hipStream_t)stream, epi);  // unsplit: no scratch

@@ -2,8 +2,10 @@
 // object of four (cq_k_*.hip); the host library embeds all four and looks
 // each kernel up by its extern "C" name with hipModuleGetFunction.
 // This object: the streaming quarter-superblock single-row GEMV cq_gemv2_*
-// (K-quants).
+// (K-quants) and the batched decode GEMV with activations loaded once per
+// workgroup cq_gemvq_* (K-quants, K <= 4096).
 #include "cq_gemv2.h"
+#include "cq_gemvq.h"
 
 #ifndef CQ_GV2_DEPTH
 #define CQ_GV2_DEPTH 3
@@ -22,3 +24,14 @@ GEMV2_FMT(q4_k, CQ_Q4_K)
 GEMV2_FMT(q5_k, CQ_Q5_K)
 GEMV2_FMT(q6_k, CQ_Q6_K)
 
+
+// Batched decode, K <= 4096: activations loaded once per workgroup, weight
+// columns streamed per wave (cq_gemvq.h).
+#define GEMVQ_KERNEL(NAME, FMT, YT) \
+  extern "C" __global__ void __launch_bounds__(64 * GVQ_MAX_WAVES) NAME(const GvqArgs a) { gemvq_body<FMT, YT>(a); }
+GEMVQ_KERNEL(cq_gemvq_q4_k_yf32, CQ_Q4_K, 0)
+GEMVQ_KERNEL(cq_gemvq_q4_k_yf16, CQ_Q4_K, 1)
+GEMVQ_KERNEL(cq_gemvq_q5_k_yf32, CQ_Q5_K, 0)
+GEMVQ_KERNEL(cq_gemvq_q5_k_yf16, CQ_Q5_K, 1)
+GEMVQ_KERNEL(cq_gemvq_q6_k_yf32, CQ_Q6_K, 0)
+GEMVQ_KERNEL(cq_gemvq_q6_k_yf16, CQ_Q6_K, 1)

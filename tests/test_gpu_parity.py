@@ -314,7 +314,7 @@ def test_graph_capture_replays(cuda, monkeypatch):
     decode of a 74-superblock Q6_K row (the row-half kernel)."""
     import torch
     monkeypatch.setenv("COMBS_GEMM2_SPLIT", "1")
-    monkeypatch.setenv("COMBS_GEMVS", "0")  # captured batched decode runs cq_gemvd_*: the eager reference too
+    monkeypatch.setenv("COMBS_GEMVS", "0")  # batched decode (k = 4096) runs cq_gemvq_*, eager and captured
     fmt, n, k = QuantFormat.Q4K, 512, 4096
     rng = np.random.default_rng(3)
     data = quantize(fmt, rng.normal(0, 0.02, (n, k)).astype(np.float32))
@@ -407,7 +407,8 @@ def test_gemv_batched_direct(cuda, monkeypatch, fmt, nt, nw, n, k, m):
     shorter than the load pipeline), m not a multiple of 4; checked against
     the oracle and bit-for-bit stable over repeated launches."""
     import torch
-    monkeypatch.setenv("COMBS_GEMVS", "0")  # cq_gemvd_*, not the LDS-shared kernel
+    monkeypatch.setenv("COMBS_GEMVQ", "0")  # cq_gemvd_*, not the column kernel
+    monkeypatch.setenv("COMBS_GEMVS", "0")  # nor the LDS-shared one
     monkeypatch.setenv("COMBS_GVD_NT", nt)
     monkeypatch.setenv("COMBS_GVD_WAVES", nw)
     data = synth(fmt, n, k)
@@ -420,6 +421,72 @@ def test_gemv_batched_direct(cuda, monkeypatch, fmt, nt, nw, n, k, m):
     O.assert_close(a, expect, 1e-3, "y32")
     O.assert_close(_run(w, x, torch.float16, torch.float16), expect, 1e-3, "y16")
     assert np.array_equal(a.view(np.uint32), _run(w, x, torch.float16, torch.float32).view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt", KQ)
+@pytest.mark.parametrize("groups", ["0", "1", "3", "7"])
+@pytest.mark.parametrize("n,k,m", [(300, 4096, 2), (35, 512, 16), (97, 3584, 7), (33, 256, 16), (500, 1792, 9),
+                                   (1000, 2048, 16), (129, 3840, 3), (4100, 4096, 13), (70, 1280, 15)])
+def test_gemv_batched_columns(cuda, monkeypatch, fmt, groups, n, k, m):
+    """Batched decode (2 <= m <= 16, fp16 x, K <= 4096) through the column
+    kernel (cq_gemvq_*): one wave per superblock column (1 to 16), ragged
+    last tile, tile ranges split over the default grid or 1, 3 or 7
+    workgroups (runs of many tiles: the two-slot ring wraps, reduction
+    chunks are full and partial), odd m, activation transits of one and of
+    two phases (m > 12, or > 14 for Q4_K / Q5_K), Q6_K rows at every even
+    byte offset of their 16-byte pieces (odd superblock counts); fp32 and
+    fp16 y and the bias epilogue, against the oracle and bit-for-bit stable
+    over repeated launches.  A weight whose size is not a multiple of 16
+    bytes takes cq_gemvd_* (the DMA reads whole pieces)."""
+    import torch
+    monkeypatch.setenv("COMBS_GEMVQ_GROUPS", groups)
+    data = synth(fmt, n, k)
+    wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
+    w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
+    x = O.x_pattern(m, k, 13, 31, 15.0, 16.0).reshape(m, k)
+    expect = O.ref_matmul(x, wd)
+    xd = torch.from_numpy(x).cuda().half()
+    kern = L.path_name(w, xd, torch.empty((m, n), device="cuda"))
+    print(f"gemvq {fmt.name} groups={groups} n={n} k={k} m={m} kernels={kern}", flush=True)
+    assert kern.startswith("cq_gemvq_" if len(data) % 16 == 0 else "cq_gemvd_")
+    a = _run(w, x, torch.float16, torch.float32)
+    O.assert_close(a, expect, 1e-3, "y32")
+    O.assert_close(_run(w, x, torch.float16, torch.float16), expect, 1e-3, "y16")
+    assert np.array_equal(a.view(np.uint32), _run(w, x, torch.float16, torch.float32).view(np.uint32))
+    b = np.linspace(-1, 1, n).astype(np.float32)
+    yb = torch.empty((m, n), device="cuda")
+    w.matmul_bias_into(xd, torch.from_numpy(b).cuda(), yb)
+    O.assert_close(yb.cpu().numpy(), expect.astype(np.float64) + b, 1e-3, "bias")
+
+
+@pytest.mark.parametrize("fmt", KQ)
+@pytest.mark.parametrize("m", [4, 16])
+def test_gemv_batched_gaussian_column_shape(cuda, fmt, m):
+    """Llama-3-8B gate / up [14336 x 4096] at batch 4 / 16 through the column
+    kernel: N(0, 0.02) quantised weights, N(0, 1) fp16 activations, against
+    the oracle, a float64 torch matmul and the direct-activation kernel."""
+    import torch
+    rng = np.random.default_rng(310 + int(fmt) + m)
+    n, k = 14336, 4096
+    data = quantize(fmt, rng.normal(0, 0.02, (n, k)).astype(np.float32))
+    wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
+    w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
+    x = rng.normal(0, 1, (m, k)).astype(np.float16).astype(np.float32)
+    xd = torch.from_numpy(x).cuda().half()
+    kern = L.path_name(w, xd, torch.empty((m, n), device="cuda"))
+    print(f"gemvq gaussian {fmt.name} m={m} kernels={kern}", flush=True)
+    assert kern.startswith("cq_gemvq_")
+    got = _run(w, x, torch.float16, torch.float32)
+    O.assert_close(got, O.ref_matmul(x, wd), 1e-3, "oracle")
+    f64 = (torch.from_numpy(x).double() @ torch.from_numpy(wd).double().T).numpy()
+    O.assert_close(got, f64, 1e-3, "f64")
+    os.environ["COMBS_GEMVQ"] = "0"
+    L.reload_options()
+    try:
+        O.assert_close(got, _run(w, x, torch.float16, torch.float32), 1e-3, "cq_gemvd")
+    finally:
+        os.environ.pop("COMBS_GEMVQ")
+        L.reload_options()
 
 
 @pytest.mark.parametrize("fmt", KQ)
@@ -493,6 +560,7 @@ def test_gemv_batched_shared(cuda, monkeypatch, fmt, split, n, k, m):
     on both the direct and the split path; against the oracle and bit-for-bit
     stable over repeated launches."""
     import torch
+    monkeypatch.setenv("COMBS_GEMVQ", "0")  # not the column kernel, which comes first
     monkeypatch.setenv("COMBS_GEMVS", "2")
     monkeypatch.setenv("COMBS_GEMVS_SPLIT", split)
     data = synth(fmt, n, k)

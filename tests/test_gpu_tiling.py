@@ -7,7 +7,9 @@ changes, so these tests require bit-identical outputs across:
   * cq_gemv1's grid size and task placement (COMBS_GEMV1_GRID,
     COMBS_GEMV1_SPREAD): a row's sum does not depend on which wave runs it;
   * cq_gemm2's tile shape (COMBS_GEMM2_NT, COMBS_GEMM2_MT);
-  * cq_gemvd's row tiles per workgroup (COMBS_GVD_NT) at a fixed wave count.
+  * cq_gemvd's row tiles per workgroup (COMBS_GVD_NT) at a fixed wave count;
+  * cq_gemvq's workgroup count (COMBS_GEMVQ_GROUPS): which workgroup runs a
+    tile, and where the reduction chunks fall, changes no sum.
 Grids of one to three workgroups also give every wave of cq_gemv1 dozens of
 tasks, so its two-slice task loop runs through every branch, for each
 format, with no epilogue, a bias epilogue and the one-launch gated gate/up;
@@ -124,7 +126,8 @@ def test_gemvd_row_tiles_bit_identical(cuda, monkeypatch, fmt, nw):
     n, k, m = 600, 4096, 9
     data, w = _weight(fmt, n, k, 950 + int(fmt))
     x = torch.from_numpy(_x(m, k, 10)).cuda().half()
-    monkeypatch.setenv("COMBS_GEMVS", "0")  # cq_gemvd_*
+    monkeypatch.setenv("COMBS_GEMVQ", "0")  # cq_gemvd_*
+    monkeypatch.setenv("COMBS_GEMVS", "0")
     monkeypatch.setenv("COMBS_GVD_WAVES", nw)
     outs = {}
     for nt in ("1", "2", "4"):
@@ -135,6 +138,30 @@ def test_gemvd_row_tiles_bit_identical(cuda, monkeypatch, fmt, nw):
         outs[nt] = _bits(y)
     for nt, v in outs.items():
         assert np.array_equal(v, outs["1"]), f"NT={nt} differs from NT=1"
+
+
+@pytest.mark.parametrize("fmt", KQ)
+@pytest.mark.parametrize("m", [3, 16])
+def test_gemvq_groups_bit_identical(cuda, monkeypatch, fmt, m):
+    """Batched decode through the column kernel: 1, 5, 64 workgroups and the
+    default grid give the same bits."""
+    import torch
+    n, k = 1300, 3584
+    data, w = _weight(fmt, n, k, 960 + int(fmt))
+    x = torch.from_numpy(_x(m, k, 11)).cuda().half()
+    outs = {}
+    for gr in ("0", "1", "5", "64"):
+        monkeypatch.setenv("COMBS_GEMVQ_GROUPS", gr)
+        assert L.path_name(w, x, torch.empty((m, n), device="cuda")).startswith("cq_gemvq_")
+        y = torch.empty((m, n), device="cuda")
+        w.matmul_into(x, y)
+        torch.cuda.synchronize()
+        outs[gr] = _bits(y)
+    wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
+    O.assert_close(outs["0"].view(np.float32), _x(m, k, 11).astype(np.float64) @ wd.T.astype(np.float64), 1e-3,
+                   "gemvq")
+    for gr, v in outs.items():
+        assert np.array_equal(v, outs["0"]), f"{gr} workgroups differ from the default grid"
 
 
 def test_dequant_rounding_blocks_bit_exact(cuda):

@@ -1,7 +1,6 @@
 // Decode GEMV for a few fp16 activation rows (2 <= m <= 16), K-quant
-// weights of at most 16 superblocks per row (K <= 4096), with every
-// activation fragment loaded once per workgroup (cq_gemvq_*):
-// y[m, n] = sum_k x[m, k] * W[n, k].
+// weights, with every activation fragment loaded once per workgroup
+// (cq_gemvq_*): y[m, n] = sum_k x[m, k] * W[n, k].
 // Replaces qmatmul.rs:881-930 (Q4_K), :1064-1117 (Q5_K) and :1184-1229
 // (Q6_K) for batched decode.
 //
@@ -14,8 +13,10 @@
 // fetched as 16-byte pieces of 16 rows at a row stride, stream poorly.
 //
 // Work mapping.
-//   - Wave u of a workgroup owns superblock column u (the workgroup has one
-//     wave per superblock of a row).  Its activations (m rows x 256 values)
+//   - Wave u of a workgroup owns superblock column cb + u of a slice of at
+//     most 16 columns (rows of up to 16 superblocks are one slice; longer
+//     rows are split into slices over blockIdx.y, whose fp32 partials
+//     cq_splitk_reduce_* adds in slice order).  Its activations (m rows x 256 values)
 //     arrive once, by LDS DMA (global_load_lds, whole 512-byte row pieces,
 //     two rows per instruction) through its ring, and are read into
 //     registers in the operand layout (8 x 16 bytes per lane), where they
@@ -49,10 +50,11 @@
 struct GvqArgs {
   const uint8_t* w;   // packed superblocks, [N rows][row_bytes]
   const _Float16* x;  // [M][K]
-  void* y;            // [M][N] fp32 or fp16
+  void* y;            // [M][N] fp32 or fp16 (no split)
+  float* part;        // split: [slices][M][N] fp32 partial sums, else null
   long long row_bytes;
   long long wbytes;   // weight bytes (the DMA never reads past them)
-  int M, N, K, units;  // units = K / 256 = waves per workgroup
+  int M, N, K, units;  // units = K / 256
   int tiles;           // ceil(N / 16)
   CqEpi epi;
 };
@@ -79,7 +81,12 @@ __device__ __forceinline__ void gemvq_body(const GvqArgs& a) {
   extern __shared__ __attribute__((aligned(16))) u4v gq_lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nw = a.units;
+  const int nw = blockDim.x >> 6;
+  // superblock columns [cb, cb + cols) of this slice (blockIdx.y); waves
+  // past the last column only take part in the reductions
+  const int cb = (int)blockIdx.y * nw;
+  const int cols = min(nw, a.units - cb);
+  const bool live = wave < cols;
   const int j = lane & 15, g = lane >> 4;
   u4v* ring = gq_lds + wave * S::WAVE_PIECES;
   // partial sums of wave w, tile tt of a chunk: TC KB after w's ring
@@ -101,7 +108,7 @@ __device__ __forceinline__ void gemvq_body(const GvqArgs& a) {
     prow[i] = q / PR;
     poff[i] = 16 * (q - prow[i] * PR);
   }
-  const size_t col = (size_t)wave * BB;
+  const size_t col = (size_t)(cb + wave) * BB;
   const size_t wlast = (size_t)a.wbytes - 16;
   auto dma = [&](int t) {  // tile t0 + t into slot t % R
     const int n0 = 16 * (t0 + t);
@@ -125,15 +132,15 @@ __device__ __forceinline__ void gemvq_body(const GvqArgs& a) {
   // row's 32 16-byte pieces, so that the 16 rows' reads of one fragment
   // fall on 16 distinct 16-byte bank groups.
   constexpr int PH = 10 - NI;
-  dma(0);
-  const int pairs = (a.M + 1) >> 1;
+  if (live) dma(0);
+  const int pairs = live ? (a.M + 1) >> 1 : 0;
   const int xr = min(j, a.M - 1), xp = xr >> 1;  // the lane's activation row and its pair
   h8 xa[8] = {};
   for (int p0 = 0; p0 < pairs; p0 += PH) {
     const int pe = min(p0 + PH, pairs);
     for (int p = p0; p < pe; p++) {
       const int r = min(2 * p + (lane & 1), a.M - 1);
-      gv3_dma16(a.x + (size_t)r * a.K + 256 * wave + 8 * ((lane >> 1) ^ p), rb + 1024 * (NI + p - p0));
+      gv3_dma16(a.x + (size_t)r * a.K + 256 * (cb + wave) + 8 * ((lane >> 1) ^ p), rb + 1024 * (NI + p - p0));
     }
     gv3_wait_vm<0>();
     if (xp >= p0 && xp < pe) {
@@ -151,7 +158,7 @@ __device__ __forceinline__ void gemvq_body(const GvqArgs& a) {
     asm volatile("" ::: "memory");
   }
 
-  for (int t = 1; t < R - 1 && t < nmine; t++) dma(t);
+  for (int t = 1; live && t < R - 1 && t < nmine; t++) dma(t);
   // Tiles in chunks of TC: each wave keeps its partial sums of a chunk
   // in registers and the chunk is added across waves afterwards, so that
   // within a chunk no wave waits for another.
@@ -160,7 +167,8 @@ __device__ __forceinline__ void gemvq_body(const GvqArgs& a) {
 #pragma unroll
     for (int tt = 0; tt < TC; tt++) {
       const int t = c0 + tt;
-      if (t < nmine) {
+      acc[tt] = f4{0, 0, 0, 0};
+      if (live && t < nmine) {
         // refill the slot of tile t - 1 (read completely) with tile
         // t + R - 1; near the end nothing is refilled and every load still
         // in flight is waited for
@@ -192,13 +200,16 @@ __device__ __forceinline__ void gemvq_body(const GvqArgs& a) {
       if (c0 + tt < nmine) {
         float v[GVQ_MAX_WAVES];
 #pragma unroll
-        for (int w2 = 0; w2 < GVQ_MAX_WAVES; w2++) v[w2] = w2 < nw ? red_at(w2, tt, r, ln) : 0.0f;
+        for (int w2 = 0; w2 < GVQ_MAX_WAVES; w2++) v[w2] = w2 < cols ? red_at(w2, tt, r, ln) : 0.0f;
         float s = v[0];
 #pragma unroll
         for (int w2 = 1; w2 < GVQ_MAX_WAVES; w2++)
-          if (w2 < nw) s += v[w2];
+          if (w2 < cols) s += v[w2];
         const int m = 4 * (ln >> 4) + r, n = 16 * (t0 + c0 + tt) + (ln & 15);
-        if (m < a.M && n < a.N) cq_store<YT>(a.y, a.epi, s, (size_t)m * a.N + n, n);
+        if (m < a.M && n < a.N) {
+          if (a.part) a.part[((size_t)blockIdx.y * a.M + m) * a.N + n] = s;
+          else cq_store<YT>(a.y, a.epi, s, (size_t)m * a.N + n, n);
+        }
       }
     }
     __syncthreads();  // partial sums read before the next chunk writes them

@@ -148,6 +148,7 @@ struct GvqArgs {
   const void* w;
   const void* x;
   void* y;
+  float* part;
   long long row_bytes;
   long long wbytes;
   int M, N, K, units, tiles;
@@ -427,7 +428,7 @@ constexpr int kUnset = -1000000;
 struct Knobs {
   int gemv_waves, gemv1, gemv1k, gemv1_grid, gemv1_i8, gemv1_prefetch2, gemv1_span, gemv1_spread,
       gemv1_wave_major, gemv2, gemv2_wpc, gemvd, gvd_nt, gvd_waves, gemm_kernel, gemm_waves, gemm2_mt,
-      gemm2_nt, gemm2_split, gateup_fused, gemvr, gemvs, gemvs_split, gemvq, gemvq_groups, gemml, gemml_nt,
+      gemm2_nt, gemm2_split, gateup_fused, gemvr, gemvs, gemvs_split, gemvq, gemvq_groups, gemvq_long, gemml, gemml_nt,
       multi_fused;
 };
 Knobs g_knobs;
@@ -464,6 +465,7 @@ void read_knobs() {
   k.gemvs_split = env_int("COMBS_GEMVS_SPLIT", 0);
   k.gemvq = env_int("COMBS_GEMVQ", 1);
   k.gemvq_groups = env_int("COMBS_GEMVQ_GROUPS", 0);
+  k.gemvq_long = env_int("COMBS_GEMVQ_LONG", 1);
   k.gemml = env_int("COMBS_GEMML", 1);
   k.gemml_nt = env_int("COMBS_GEMML_NT", 0);
   k.multi_fused = env_int("COMBS_MULTI_FUSED", 1);
@@ -764,25 +766,32 @@ static cq_status launch_gemvs(DeviceModule* dm, const cq_weight* w, const void* 
 }
 
 // Batched decode with every activation fragment loaded once per workgroup
-// (cq_gemvq_*, K-quants, 2 <= m <= 16, at most 16 superblocks per row):
-// one wave per superblock column, workgroups over balanced ranges of 16-row
-// tiles, at most as many workgroups as fit on the compute units at once.
-// LDS per wave: 10 KB, a DMA ring of two slots (3 KB for Q4_K / Q5_K, 4 KB
-// for Q6_K), which also carries the activation transit, and the rest for
-// the partial sums of 1 KB per tile of a reduction chunk.
-// Needs the weight, its size and the activations 16-byte aligned (whole
-// 16-byte DMA pieces).
+// (cq_gemvq_*, K-quants, 2 <= m <= 16): one wave per superblock column of a
+// slice of at most 16 columns (rows of more superblocks are cut into
+// ceil(units / 16) slices of equal length over blockIdx.y, and
+// cq_splitk_reduce_* adds their fp32 partials in slice order), workgroups
+// over balanced ranges of 16-row tiles, at most as many workgroups as fit
+// on the compute units at once.  LDS per wave: 10 KB, a DMA ring of two
+// slots (3 KB for Q4_K / Q5_K, 4 KB for Q6_K), which also carries the
+// activation transit, and the rest for the partial sums of 1 KB per tile of
+// a reduction chunk.  Needs the weight, its size and the activations
+// 16-byte aligned (whole 16-byte DMA pieces).  The slices' partials come
+// from the stream-ordered pool, or, while capturing and in
+// cq_matmul_noalloc, from the device's fixed buffer; when neither is to be
+// had (*declined set, nothing launched) the caller takes cq_gemvd_*.
 static bool gemvq_fits(const cq_weight* w, const void* x) {
-  return gemvs_fits(w) && w->k / 256 <= 16 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+  return gemvs_fits(w) && w->k / 256 <= 128 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
 }
 static int gemvq_lds_bytes(int nw) { return nw * 10 * 1024; }
 static cq_status launch_gemvq(DeviceModule* dm, const cq_weight* w, const void* x, int64_t m, void* y, int yt,
-                              hipStream_t s, const CqEpi& epi) {
+                              hipStream_t s, const CqEpi& epi, bool* declined) {
+  *declined = false;
   const int fi = fmt_index(w->format);
   GvqArgs a{};
   a.w = w->dev;
   a.x = x;
   a.y = y;
+  a.part = nullptr;
   a.row_bytes = (long long)(w->nbytes / (size_t)w->n);
   a.wbytes = (long long)w->nbytes;
   a.M = (int)m;
@@ -793,12 +802,51 @@ static cq_status launch_gemvq(DeviceModule* dm, const cq_weight* w, const void* 
   const long long tiles = (w->n + 15) / 16;
   if (tiles > 0x7fffffffLL) return fail(CQ_ERR_BAD_SHAPE, "grid too large (n=%lld)", (long long)w->n);
   a.tiles = (int)tiles;
-  const int lds = gemvq_lds_bytes(a.units);
-  const int per_cu = std::max(1, std::min(160 * 1024 / lds, 16 / a.units));
-  long long groups = knobs().gemvq_groups > 0 ? knobs().gemvq_groups : (long long)dm->cus * per_cu;
+  const int slices = (a.units + 15) / 16;
+  const int nw = (a.units + slices - 1) / slices;  // columns (waves) per slice
+  const int lds = gemvq_lds_bytes(nw);
+  const int per_cu = std::max(1, std::min(160 * 1024 / lds, 16 / nw));
+  long long groups = knobs().gemvq_groups > 0 ? knobs().gemvq_groups
+                                              : std::max(1LL, (long long)dm->cus * per_cu / slices);
   groups = std::min(groups, tiles);
+  const size_t part_bytes = slices > 1 ? (size_t)slices * m * w->n * 4 : 0;
+  const FixedScratch* fixed = g_fixed;
+  FixedScratch cap_fs{nullptr, 0};
+  if (part_bytes && !fixed && !g_plan) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    HIP_TRY(hipStreamIsCapturing(s, &cs));
+    if (cs != hipStreamCaptureStatusNone) {
+      if (cq_scratch_device_ptr(&cap_fs.ptr, &cap_fs.bytes) != hipSuccess) {
+        (void)hipGetLastError();
+        *declined = true;
+        return CQ_OK;
+      }
+      fixed = &cap_fs;
+    }
+  }
+  if (part_bytes && fixed && part_bytes > fixed->bytes) {
+    *declined = true;
+    return CQ_OK;
+  }
+  void* ws = nullptr;
+  if (part_bytes) {
+    if (fixed) ws = fixed->ptr;
+    else if (!g_plan) HIP_TRY(hipMallocAsync(&ws, part_bytes, s));
+    a.part = (float*)ws;
+  }
   void* params[] = {&a};
-  HIP_TRY(klaunch(dm, dm->gemvq[fi][yt], (unsigned)groups, 1, 1, 64 * a.units, (unsigned)lds, s, params));
+  hipError_t e = klaunch(dm, dm->gemvq[fi][yt], (unsigned)groups, (unsigned)slices, 1, 64 * nw, (unsigned)lds, s,
+                         params);
+  if (e == hipSuccess && part_bytes) {
+    long long mn = m * w->n;
+    int n = (int)w->n;
+    int sl = slices;
+    CqEpi ep = epi;
+    void* rp[] = {&a.part, &y, &sl, &mn, &n, &ep};
+    e = klaunch(dm, dm->reduce[yt], (unsigned)((mn + 255) / 256), 1, 1, 256, 0, s, rp);
+  }
+  if (ws && !fixed) HIP_TRY(hipFreeAsync(ws, s));
+  if (e != hipSuccess) return fail(CQ_ERR_HIP, "batched decode launch: %s", hipGetErrorString(e));
   return CQ_OK;
 }
 
@@ -1253,8 +1301,12 @@ static cq_status matmul_impl(const cq_weight* w, const void* x, int x_dtype, int
     if (gemv1k_fits(w) && knobs().gemv1k) return launch_gemv1k(dm, w, x, y, yt, (hipStream_t)stream, epi);
     if (kq && w->k / 256 <= 64 && gemv2_fits(w)) return launch_gemv2(dm, w, x, y, yt, (hipStream_t)stream, epi);
   }
-  if (kq && !xt && m >= 2 && m <= 16 && knobs().gemvq && gemvq_fits(w, x))
-    return launch_gemvq(dm, w, x, m, y, yt, (hipStream_t)stream, epi);
+  if (kq && !xt && m >= 2 && m <= 16 && knobs().gemvq && gemvq_fits(w, x) &&
+      (w->k / 256 <= 16 || knobs().gemvq == 2 || knobs().gemvq_long)) {
+    bool declined;
+    const cq_status st = launch_gemvq(dm, w, x, m, y, yt, (hipStream_t)stream, epi, &declined);
+    if (!declined) return st;
+  }
   if (kq && !xt && m >= 2 && m <= 16 && gemvs_fits(w)) {
     if (knobs().gemvs == 1 && w->n >= (int64_t)16 * kGvsWaves * dm->cus)
       return launch_gemvs(dm, w, x, m, y, yt, (hipStream_t)stream, epi);  // unsplit: no scratch

@@ -395,6 +395,50 @@ def test_graph_capture_prefill_split(cuda, fmt, n, k, m):
         assert torch.equal(y, ref), rep
 
 
+@pytest.mark.parametrize("fmt,n,k,m", [(QuantFormat.Q4K, 4096, 14336, 16), (QuantFormat.Q6K, 300, 18944, 5),
+                                        (QuantFormat.Q5K, 1000, 8192, 9)])
+def test_graph_capture_batched_slices(cuda, fmt, n, k, m):
+    """Batched decode of rows longer than 16 superblocks captured into a HIP
+    graph: the captured column kernel takes its slice partials from the
+    device's fixed scratch (no allocation in the graph) and must give the
+    eager launch's bits (partials from the stream-ordered pool) on every
+    replay, with eager batched decode and a no-allocation call (which
+    overwrites the fixed buffer) between the replays."""
+    import torch
+    rng = np.random.default_rng(60 + int(fmt) + m)
+    data = quantize(fmt, rng.normal(0, 0.02, (n, k)).astype(np.float32))
+    w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
+    wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
+    x = torch.from_numpy(rng.normal(0, 1, (m, k)).astype(np.float16)).cuda()
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    kern = L.kernels(w, L.CQ_F16, m, L.CQ_F32)
+    print(f"captured batched {fmt.name} [{n}x{k}] m={m} kernels={kern}", flush=True)
+    assert kern.startswith("cq_gemvq_") and "splitk" in kern
+    w.matmul_into(x, y)
+    torch.cuda.synchronize()
+    ref = y.clone()
+    O.assert_close(ref.cpu().numpy(), x.double().cpu().numpy() @ wd.astype(np.float64).T, 1e-3, "eager")
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            w.matmul_into(x, y)
+    torch.cuda.current_stream().wait_stream(s)
+    x2 = torch.from_numpy(rng.normal(0, 1, (m - 1 if m > 2 else 2, k)).astype(np.float16)).cuda()
+    y2 = torch.empty((x2.shape[0], n), dtype=torch.float32, device="cuda")
+    for rep in range(4):
+        y.fill_(float("nan"))
+        w.matmul_into(x2, y2)  # eager batched decode between replays
+        st = L.lib().cq_matmul_noalloc(w.handle, x2.data_ptr(), L.CQ_F16, x2.shape[0], y2.data_ptr(), L.CQ_F32,
+                                       torch.cuda.current_stream().cuda_stream)
+        assert st == L.CQ_OK, L.last_error()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, ref), rep
+
+
 @pytest.mark.parametrize("fmt", KQ)
 @pytest.mark.parametrize("nt", ["1", "2", "4"])
 @pytest.mark.parametrize("nw", ["1", "3", "8"])
@@ -426,11 +470,14 @@ def test_gemv_batched_direct(cuda, monkeypatch, fmt, nt, nw, n, k, m):
 @pytest.mark.parametrize("fmt", KQ)
 @pytest.mark.parametrize("groups", ["0", "1", "3", "7"])
 @pytest.mark.parametrize("n,k,m", [(300, 4096, 2), (35, 512, 16), (97, 3584, 7), (33, 256, 16), (500, 1792, 9),
-                                   (1000, 2048, 16), (129, 3840, 3), (4100, 4096, 13), (70, 1280, 15)])
+                                   (1000, 2048, 16), (129, 3840, 3), (4100, 4096, 13), (70, 1280, 15),
+                                   (70, 14336, 4), (300, 18944, 9), (33, 4352, 16), (129, 8192, 3)])
 def test_gemv_batched_columns(cuda, monkeypatch, fmt, groups, n, k, m):
-    """Batched decode (2 <= m <= 16, fp16 x, K <= 4096) through the column
-    kernel (cq_gemvq_*): one wave per superblock column (1 to 16), ragged
-    last tile, tile ranges split over the default grid or 1, 3 or 7
+    """Batched decode (2 <= m <= 16, fp16 x) through the column kernel
+    (cq_gemvq_*): one wave per superblock column (1 to 16), rows of more
+    than 16 superblocks cut into slices (4 x 14, 5 x 15 with an idle wave in
+    the last, 2 x 9 with one idle, 2 x 16) whose partials are summed in
+    order, ragged last tile, tile ranges split over the default grid or 1, 3 or 7
     workgroups (runs of many tiles: the two-slot ring wraps, reduction
     chunks are full and partial), odd m, activation transits of one and of
     two phases (m > 12, or > 14 for Q4_K / Q5_K), Q6_K rows at every even
@@ -444,7 +491,11 @@ def test_gemv_batched_columns(cuda, monkeypatch, fmt, groups, n, k, m):
     wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
     w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
     x = O.x_pattern(m, k, 13, 31, 15.0, 16.0).reshape(m, k)
-    expect = O.ref_matmul(x, wd)
+    # above 4096 values the synthetic rows cancel far enough that the
+    # oracle's sequential fp32 sum is itself ~1e-3 off: float64 of its
+    # (bit-exact) dequant there (Q6_K [300 x 18944]: fp32 1.95363, float64
+    # 1.95614 at [2, 212])
+    expect = O.ref_matmul(x, wd) if k <= 4096 else x.astype(np.float64) @ wd.astype(np.float64).T
     xd = torch.from_numpy(x).cuda().half()
     kern = L.path_name(w, xd, torch.empty((m, n), device="cuda"))
     print(f"gemvq {fmt.name} groups={groups} n={n} k={k} m={m} kernels={kern}", flush=True)
@@ -493,8 +544,9 @@ def test_gemv_batched_gaussian_column_shape(cuda, fmt, m):
 @pytest.mark.parametrize("m", [4, 16])
 def test_gemv_batched_gaussian_llama_shape(cuda, fmt, m):
     """BASELINE config 3 shape [4096 x 14336] at batch 4 / 16: N(0, 0.02)
-    quantised weights, N(0, 1) fp16 activations, against the oracle, the
-    16-row LDS-staged MFMA kernel and a float64 torch matmul."""
+    quantised weights, N(0, 1) fp16 activations, against the oracle, a
+    float64 torch matmul and, after the column kernel (four slices), the
+    direct-activation kernel and the 16-row LDS-staged MFMA kernel."""
     import torch
     rng = np.random.default_rng(300 + int(fmt) + m)
     n, k = 4096, 14336
@@ -507,14 +559,18 @@ def test_gemv_batched_gaussian_llama_shape(cuda, fmt, m):
     O.assert_close(got, O.ref_matmul(x, wd), 1e-3, "oracle")
     f64 = (torch.from_numpy(x).double() @ torch.from_numpy(wd).double().T).numpy()
     O.assert_close(got, f64, 1e-3, "f64")
-    for knob in ("COMBS_GEMVS", "COMBS_GEMVD"):  # the direct-activation kernel, then the 16-row MFMA GEMV
-        os.environ[knob] = "0"
+    assert L.kernels(w, L.CQ_F16, m, L.CQ_F32).startswith("cq_gemvq_")
+    knobs = ("COMBS_GEMVQ", "COMBS_GEMVS", "COMBS_GEMVD")  # then direct-activation, then the 16-row MFMA GEMV
+    try:
+        for knob in knobs:
+            os.environ[knob] = "0"
+            L.reload_options()
+            old = _run(w, x, torch.float16, torch.float32)
+            O.assert_close(got, old, 1e-3, f"with {knob}=0")
+    finally:
+        for knob in knobs:
+            os.environ.pop(knob, None)
         L.reload_options()
-        old = _run(w, x, torch.float16, torch.float32)
-        O.assert_close(got, old, 1e-3, f"with {knob}=0")
-    os.environ.pop("COMBS_GEMVS")
-    os.environ.pop("COMBS_GEMVD")
-    L.reload_options()
 
 
 @pytest.mark.parametrize("fmt", [QuantFormat.Q4K, QuantFormat.Q5K, QuantFormat.Q6K, QuantFormat.Q4_0, QuantFormat.Q8_0])

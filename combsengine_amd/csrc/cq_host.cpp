@@ -242,6 +242,17 @@ struct DeviceModule {
   hipFunction_t gemml[kNumFormats][2][2] = {};  // 32-value formats only: [format][NT - 1][y f16]
   hipFunction_t gemvr[2][4] = {};  // Q4_K rows split across lanes: [y f16][log2 activation pieces per thread]
   int cus = 0;                        // compute units of the device
+  // Scratch kept across calls (batched decode slice partials): grown on
+  // demand, never freed before the process ends; `ev` is recorded on the
+  // stream of each use, and a call on another stream waits for it first.
+  struct {
+    std::mutex mu;
+    void* ptr = nullptr;
+    size_t bytes = 0;
+    hipEvent_t ev = nullptr;
+    hipStream_t last = nullptr;
+    bool used = false;
+  } kept;
 };
 DeviceModule g_dev[kMaxDevices];
 
@@ -419,6 +430,34 @@ cq_status device_module(DeviceModule** out) {
   if (d.status != CQ_OK) return fail(d.status, "device %d: %s", dev, d.err.c_str());
   *out = &d;
   return CQ_OK;
+}
+
+// Runs `enqueue(ptr)` with the device's kept scratch of at least `bytes`
+// bytes, ordered after the previous use of that scratch on any stream: no
+// per-call allocation (a stream-ordered allocate / free pair costs ~17 us
+// of host time per call on this runtime, more than a decode launch's
+// device time).  Not for use while capturing (the event record and wait
+// would become graph nodes).
+template <typename F>
+static hipError_t with_kept_scratch(DeviceModule* dm, hipStream_t s, size_t bytes, F enqueue) {
+  auto& k = dm->kept;
+  std::lock_guard<std::mutex> lock(k.mu);
+  hipError_t e;
+  if (!k.ev && (e = hipEventCreateWithFlags(&k.ev, hipEventDisableTiming)) != hipSuccess) return e;
+  if (k.used && k.last != s && (e = hipStreamWaitEvent(s, k.ev, 0)) != hipSuccess) return e;
+  if (bytes > k.bytes) {
+    if (k.ptr && (e = hipFreeAsync(k.ptr, s)) != hipSuccess) return e;
+    k.ptr = nullptr;
+    k.bytes = 0;
+    const size_t grow = std::max(bytes, (size_t)4 << 20);
+    if ((e = hipMallocAsync(&k.ptr, grow, s)) != hipSuccess) return e;
+    k.bytes = grow;
+  }
+  e = enqueue(k.ptr);
+  const hipError_t r = hipEventRecord(k.ev, s);
+  k.last = s;
+  k.used = true;
+  return e != hipSuccess ? e : r;
 }
 
 // Tuning and A/B knobs (COMBS_* environment variables), read once at the
@@ -776,8 +815,8 @@ static cq_status launch_gemvs(DeviceModule* dm, const cq_weight* w, const void* 
 // activation transit, and the rest for the partial sums of 1 KB per tile of
 // a reduction chunk.  Needs the weight, its size and the activations
 // 16-byte aligned (whole 16-byte DMA pieces).  The slices' partials come
-// from the stream-ordered pool, or, while capturing and in
-// cq_matmul_noalloc, from the device's fixed buffer; when neither is to be
+// from the device's kept scratch (with_kept_scratch), or, while capturing
+// and in cq_matmul_noalloc, from its fixed buffer; when that is not to be
 // had (*declined set, nothing launched) the caller takes cq_gemvd_*.
 static bool gemvq_fits(const cq_weight* w, const void* x) {
   return gemvs_fits(w) && w->k / 256 <= 128 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
@@ -828,24 +867,24 @@ static cq_status launch_gemvq(DeviceModule* dm, const cq_weight* w, const void* 
     *declined = true;
     return CQ_OK;
   }
-  void* ws = nullptr;
-  if (part_bytes) {
-    if (fixed) ws = fixed->ptr;
-    else if (!g_plan) HIP_TRY(hipMallocAsync(&ws, part_bytes, s));
+  auto launch_all = [&](void* ws) -> hipError_t {
     a.part = (float*)ws;
-  }
-  void* params[] = {&a};
-  hipError_t e = klaunch(dm, dm->gemvq[fi][yt], (unsigned)groups, (unsigned)slices, 1, 64 * nw, (unsigned)lds, s,
-                         params);
-  if (e == hipSuccess && part_bytes) {
+    void* params[] = {&a};
+    hipError_t e = klaunch(dm, dm->gemvq[fi][yt], (unsigned)groups, (unsigned)slices, 1, 64 * nw, (unsigned)lds, s,
+                           params);
+    if (e != hipSuccess || !part_bytes) return e;
     long long mn = m * w->n;
     int n = (int)w->n;
     int sl = slices;
     CqEpi ep = epi;
     void* rp[] = {&a.part, &y, &sl, &mn, &n, &ep};
-    e = klaunch(dm, dm->reduce[yt], (unsigned)((mn + 255) / 256), 1, 1, 256, 0, s, rp);
-  }
-  if (ws && !fixed) HIP_TRY(hipFreeAsync(ws, s));
+    return klaunch(dm, dm->reduce[yt], (unsigned)((mn + 255) / 256), 1, 1, 256, 0, s, rp);
+  };
+  hipError_t e;
+  if (!part_bytes) e = launch_all(nullptr);
+  else if (fixed) e = launch_all(fixed->ptr);
+  else if (g_plan) e = launch_all(nullptr);
+  else e = with_kept_scratch(dm, s, part_bytes, launch_all);
   if (e != hipSuccess) return fail(CQ_ERR_HIP, "batched decode launch: %s", hipGetErrorString(e));
   return CQ_OK;
 }

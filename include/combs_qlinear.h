@@ -103,11 +103,12 @@ const void* cq_weight_device_ptr(const cq_weight* w);
  * QuantLinearOp::forward it serves (qlinear.rs:58).  x: device, x_dtype
  * CQ_F16 or CQ_F32; y: device, caller-allocated, y_dtype CQ_F32 or CQ_F16.
  * fp32 activations must be finite and below 65504 in magnitude (they are fed
- * to the fp16 matrix cores as a hi+lo pair).  Prefill (m > 16) takes
- * stream-ordered scratch; while the stream is being captured into a HIP
- * graph it takes the device's fixed array instead (see cq_matmul_noalloc),
- * which graphs captured this way share: replays that overlap on one device
- * race. */
+ * to the fp16 matrix cores as a hi+lo pair).  Prefill (m > 16) and
+ * batched decode (2 <= m <= 16) of rows longer than 16 superblocks take
+ * stream-ordered scratch (activation sums, split partials); while the
+ * stream is being captured into a HIP graph they take the device's fixed
+ * array instead (see cq_matmul_noalloc), which graphs captured this way
+ * share: replays that overlap on one device race. */
 cq_status cq_matmul(const cq_weight* w, const void* x, int x_dtype, int64_t m, void* y, int y_dtype,
                     void* stream);
 
@@ -165,7 +166,8 @@ cq_status cq_quantize(int format, const float* src, int64_t rows, int64_t k, voi
  * capture, serving loops, harnesses that forbid hipMalloc).  Same
  * arguments, kernels and results as cq_matmul; where cq_matmul takes
  * stream-ordered scratch (the prefill GEMM's activation sums and split-K
- * partials) this uses a fixed 32 MiB device array that the library holds
+ * partials, the batched decode's slice partials of long rows) this uses a
+ * fixed 32 MiB device array that the library holds
  * on each device until the process ends, shrinking the K split until the
  * partials fit; a prefill whose activation sums alone (m * K / 8 bytes for
  * Q4_K / Q5_K) exceed it returns CQ_ERR_BAD_SHAPE.  Every call on a device

@@ -439,6 +439,43 @@ def test_graph_capture_batched_slices(cuda, fmt, n, k, m):
         assert torch.equal(y, ref), rep
 
 
+def test_batched_slices_two_streams(cuda):
+    """The batched decode's slice partials live in a per-device scratch kept
+    across calls: calls alternating between two streams with no host
+    synchronisation (each waits for the other stream's last use), growing
+    the scratch midway (a wider weight, then m = 16), give every output the
+    bits of the same call made alone."""
+    import torch
+    rng = np.random.default_rng(71)
+    ws = []
+    for n, k in ((500, 8192), (3000, 14336)):
+        data = quantize(QuantFormat.Q4K, rng.normal(0, 0.02, (n, k)).astype(np.float32))
+        ws.append(QuantWeight.from_gguf_bytes(QuantFormat.Q4K, data, n, k))
+    calls = []  # (weight, x, y)
+    for i in range(12):
+        w = ws[0] if i < 6 else ws[1]
+        m = 4 if i < 9 else 16
+        calls.append((w, torch.from_numpy(rng.normal(0, 1, (m, w.k())).astype(np.float16)).cuda(),
+                      torch.empty((m, w.n_out()), device="cuda")))
+    assert "splitk" in L.kernels(ws[1], L.CQ_F16, 16, L.CQ_F32)
+    refs = []
+    for w, x, y in calls:
+        w.matmul_into(x, y)
+        torch.cuda.synchronize()
+        refs.append(y.clone())
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    for _, _, y in calls:
+        y.fill_(float("nan"))
+    torch.cuda.synchronize()
+    for i, (w, x, y) in enumerate(calls):
+        with torch.cuda.stream(streams[i % 2]):
+            w.matmul_into(x, y)
+    torch.cuda.synchronize()
+    for i, (_, _, y) in enumerate(calls):
+        assert torch.equal(y, refs[i]), i
+
+
 @pytest.mark.parametrize("fmt", KQ)
 @pytest.mark.parametrize("nt", ["1", "2", "4"])
 @pytest.mark.parametrize("nw", ["1", "3", "8"])

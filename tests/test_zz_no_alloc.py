@@ -6,8 +6,10 @@ Two calls in a row on each weight, the second with fewer activation rows, so
 the second reuses the scratch the first left behind.  Checked bit for bit
 against cq_matmul (same kernels and K split) and against float64 over the
 oracle's dequant (|y - y_ref| <= 1e-3 * max(|y_ref|, 1)); the decode path
-(no scratch) is checked too, and a prefill whose activation sums exceed the
-scratch is rejected with CQ_ERR_BAD_SHAPE."""
+(no scratch at m = 1 and for rows of at most 16 superblocks; for longer
+rows the batched decode's slice partials, m = 16 then 5, 9 then 3) is
+checked too, and a prefill whose activation sums exceed the scratch is
+rejected with CQ_ERR_BAD_SHAPE."""
 import numpy as np
 import pytest
 
@@ -27,7 +29,8 @@ def _call(fn, w, x, y):
 
 
 @pytest.mark.parametrize("fmt,n,k,ms", [(F.Q4K, 512, 3584, (512, 130)), (F.Q5K, 1000, 2048, (300, 40)),
-                                        (F.Q6K, 512, 3584, (512, 64)), (F.Q4K, 300, 4096, (1, 9))])
+                                        (F.Q6K, 512, 3584, (512, 64)), (F.Q4K, 300, 4096, (1, 9)),
+                                        (F.Q6K, 700, 14336, (16, 5)), (F.Q4K, 300, 18944, (9, 3))])
 def test_noalloc_matches_matmul(cuda, fmt, n, k, ms):
     import torch
     assert L.lib().cq_device_init() == L.CQ_OK, L.last_error()

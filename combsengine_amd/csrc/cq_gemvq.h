@@ -59,25 +59,91 @@ struct GvqArgs {
   CqEpi epi;
 };
 
-// 16-byte pieces of one row's superblock in a slot and DMA instructions per
-// slot (64 pieces each); two slots per wave.
+// A column is 256 values of a row: one K-quant superblock, or 8 blocks of a
+// 32-value format.  Per wave a ring of two slots, each 16 rows x PR
+// 16-byte pieces (a column from the 16-byte boundary at or below its start;
+// DMA lanes past the last piece are masked off), rounded up to 256 bytes,
+// then TC KB of partial sums, within a 10 KB share of the 160 KB.
 template <int FMT>
 struct GvqShape {
-  static constexpr int BB = FmtTraits<FMT>::bytes;
-  static constexpr int PR = BB % 16 == 0 ? BB / 16 : (BB + 15) / 16 + 1;
-  static constexpr int NI = (16 * PR + 63) / 64;
+  static constexpr bool KQ = FmtTraits<FMT>::vals == 256;
+  static constexpr int CB = KQ ? FmtTraits<FMT>::bytes : 8 * FmtTraits<FMT>::bytes / LB;  // column bytes per row
+  static constexpr int PR = CB % 16 == 0 ? CB / 16 : (CB + 15) / 16 + 1;
+  static constexpr int P = 16 * PR;                 // pieces per slot
+  static constexpr int NI = (P + 63) / 64;          // DMA instructions per slot
+  static constexpr int SLOT = (16 * P + 255) / 256 * 256;  // bytes
   static constexpr int R = 2;
-  // tiles per cross-wave reduction: their partial sums live in registers
-  // and then 1 KB per wave and tile of LDS, whatever of a wave's 10 KB
-  // share of the 160 KB the ring leaves
-  static constexpr int TC = 10 - R * NI;
-  static constexpr int WAVE_PIECES = 10 * 64;  // u4v per wave: ring, then partial sums
+  // tiles per cross-wave reduction (their partial sums in registers, then
+  // LDS): what LDS leaves, at most 4 (2 for Q6_K's larger decode state)
+  static constexpr int TC_LDS = (10240 - R * SLOT) / 1024;
+  static constexpr int TC = TC_LDS < (FMT == CQ_Q6_K ? 2 : 4) ? TC_LDS : (FMT == CQ_Q6_K ? 2 : 4);
+  // activation row pairs of 1 KB that slot 1 and the partial sums carry
+  static constexpr int PH = (10240 - SLOT) / 1024;
+  static constexpr int WAVE_BYTES = 10240;
+  static_assert(TC >= 1 && PH >= 1, "column too large for the LDS share");
 };
+
+// A fragment s of lane group g of a column, as 16-byte pieces p0 (and, for
+// the 4-bit / 5-bit legacy formats, the second half of a split fragment at
+// byte offset o1 of piece p1): the k layout the format's B operands use.
+template <int FMT>
+__device__ __forceinline__ void gvq_apos(int g, int s, int& p0, int& o0, int& p1, int& o1) {
+  if constexpr (FmtTraits<FMT>::vals == 256) {
+    p0 = (gvd_abase<FMT>(g) + gvd_aoff<FMT>(s)) >> 3;  // 8 values = one piece
+    o0 = 0;
+    p1 = -1;
+    o1 = 0;
+  } else if constexpr (FMT == CQ_Q8_0) {
+    p0 = 4 * s + g;  // block s, k = 32 s + 8 g .. + 7
+    o0 = 0;
+    p1 = -1;
+    o1 = 0;
+  } else {
+    // block s: k = 32 s + 4 g .. + 3, then 32 s + 16 + 4 g .. + 3
+    p0 = 4 * s + (g >> 1);
+    o0 = 8 * (g & 1);
+    p1 = 4 * s + 2 + (g >> 1);
+    o1 = 8 * (g & 1);
+  }
+}
+
+// One column of one 16-row tile against the lane's 8 A fragments (legacy:
+// block s meets fragment s; every block's fp16 scale, and the affine
+// formats' min times the block's activation sum, applied to fp32 results).
+template <int FMT>
+__device__ __forceinline__ f4 gvq_column(const uint8_t* wp, const h8 (&xa)[8], int g) {
+  if constexpr (FmtTraits<FMT>::vals == 256) {
+    typename FmtTraits<FMT>::Frag f;
+    load_unit<FMT>(f, wp, g, 0);
+    return gvd_superblock<FMT>(f, xa, g);
+  } else {
+    f4 acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      typename FmtTraits<FMT>::Frag f;
+      load_unit<FMT>(f, wp + h * LB * FmtTraits<FMT>::bytes / LB, g, LB);
+#pragma unroll
+      for (int i = 0; i < LB; i++) {
+        const h8 b = legacy_b(f, i, g);
+        const h8 a = xa[LB * h + i];
+        if constexpr (FMT == CQ_Q4_1 || FMT == CQ_Q5_1) {
+          affine_block<0>(A8<0>{a, a}, b, legacy_d(f, i), acc);
+        } else {
+          const f4 c = mfma(a, b, f4{0, 0, 0, 0});
+          const float d = f16_bits_to_f32(legacy_d(f, i));
+#pragma unroll
+          for (int r = 0; r < 4; r++) acc[r] = __builtin_fmaf(d, c[r], acc[r]);
+        }
+      }
+    }
+    return acc;
+  }
+}
 
 template <int FMT, int YT>
 __device__ __forceinline__ void gemvq_body(const GvqArgs& a) {
   typedef GvqShape<FMT> S;
-  constexpr int BB = S::BB, PR = S::PR, NI = S::NI, R = S::R, TC = S::TC;
+  constexpr int CB = S::CB, PR = S::PR, P = S::P, NI = S::NI, SLOT = S::SLOT, R = S::R, TC = S::TC;
   extern __shared__ __attribute__((aligned(16))) u4v gq_lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -88,10 +154,10 @@ __device__ __forceinline__ void gemvq_body(const GvqArgs& a) {
   const int cols = min(nw, a.units - cb);
   const bool live = wave < cols;
   const int j = lane & 15, g = lane >> 4;
-  u4v* ring = gq_lds + wave * S::WAVE_PIECES;
+  u4v* ring = gq_lds + wave * (S::WAVE_BYTES / 16);
   // partial sums of wave w, tile tt of a chunk: TC KB after w's ring
   auto red_at = [&](int w, int tt, int r, int ln) -> float& {
-    return ((float*)(gq_lds + w * S::WAVE_PIECES + R * NI * 64))[(tt * 4 + r) * 64 + ln];
+    return ((float*)((uint8_t*)gq_lds + w * S::WAVE_BYTES + R * SLOT))[(tt * 4 + r) * 64 + ln];
   };
   const uint32_t rb = gv3_lds_addr(ring);
   // this workgroup's tiles [t0, t0 + nmine)
@@ -100,23 +166,25 @@ __device__ __forceinline__ void gemvq_body(const GvqArgs& a) {
   const int nmine = (int)((long long)(blockIdx.x + 1) * a.tiles / G) - t0;
 
   // Weight pieces of this lane: piece q = 64 i + lane of a slot is piece
-  // q % PR of row q / PR's superblock (from its 16-byte boundary).
+  // q % PR of row q / PR's column (from its 16-byte boundary); q >= P is
+  // not loaded.
   int prow[NI], poff[NI];
 #pragma unroll
   for (int i = 0; i < NI; i++) {
-    const int q = min(64 * i + lane, 16 * PR - 1);
+    const int q = min(64 * i + lane, P - 1);
     prow[i] = q / PR;
     poff[i] = 16 * (q - prow[i] * PR);
   }
-  const size_t col = (size_t)(cb + wave) * BB;
+  const size_t col = (size_t)(cb + wave) * CB;
   const size_t wlast = (size_t)a.wbytes - 16;
   auto dma = [&](int t) {  // tile t0 + t into slot t % R
     const int n0 = 16 * (t0 + t);
-    const uint32_t lb = rb + 1024 * NI * (t % R);
+    const uint32_t lb = rb + SLOT * (t % R);
 #pragma unroll
     for (int i = 0; i < NI; i++) {
       const size_t s = (size_t)min(n0 + prow[i], a.N - 1) * (size_t)a.row_bytes + col;
-      gv3_dma16(a.w + min((s & ~(size_t)15) + poff[i], wlast), lb + 1024 * i);
+      if (P % 64 == 0 || i + 1 < NI || 64 * i + lane < P)
+        gv3_dma16(a.w + min((s & ~(size_t)15) + poff[i], wlast), lb + 1024 * i);
     }
   };
   // the lane's row within a slot: byte offset of its superblock
@@ -131,7 +199,7 @@ __device__ __forceinline__ void gemvq_body(const GvqArgs& a) {
   // (even lanes) and 2p + 1 (odd lanes), piece (lane >> 1) ^ p of each
   // row's 32 16-byte pieces, so that the 16 rows' reads of one fragment
   // fall on 16 distinct 16-byte bank groups.
-  constexpr int PH = 10 - NI;
+  constexpr int PH = S::PH;
   if (live) dma(0);
   const int pairs = live ? (a.M + 1) >> 1 : 0;
   const int xr = min(j, a.M - 1), xp = xr >> 1;  // the lane's activation row and its pair
@@ -140,15 +208,21 @@ __device__ __forceinline__ void gemvq_body(const GvqArgs& a) {
     const int pe = min(p0 + PH, pairs);
     for (int p = p0; p < pe; p++) {
       const int r = min(2 * p + (lane & 1), a.M - 1);
-      gv3_dma16(a.x + (size_t)r * a.K + 256 * (cb + wave) + 8 * ((lane >> 1) ^ p), rb + 1024 * (NI + p - p0));
+      gv3_dma16(a.x + (size_t)r * a.K + 256 * (cb + wave) + 8 * ((lane >> 1) ^ p), rb + SLOT + 1024 * (p - p0));
     }
     gv3_wait_vm<0>();
     if (xp >= p0 && xp < pe) {
-      const uint8_t* base = (const uint8_t*)ring + 1024 * (NI + xp - p0) + 16 * (xr & 1);
+      const uint8_t* base = (const uint8_t*)ring + SLOT + 1024 * (xp - p0) + 16 * (xr & 1);
 #pragma unroll
       for (int s = 0; s < 8; s++) {
-        const int piece = (gvd_abase<FMT>(g) + gvd_aoff<FMT>(s)) >> 3;  // fragment s of lane group g
-        xa[s] = __builtin_bit_cast(h8, ld_u128(base + 32 * (piece ^ xp)));
+        int p0s, o0s, p1s, o1s;
+        gvq_apos<FMT>(g, s, p0s, o0s, p1s, o1s);  // fragment s of lane group g
+        if (p1s < 0) {
+          xa[s] = __builtin_bit_cast(h8, ld_u128(base + 32 * (p0s ^ xp)));
+        } else {
+          const u2v lo = ld_u64(base + 32 * (p0s ^ xp) + o0s), hi = ld_u64(base + 32 * (p1s ^ xp) + o1s);
+          xa[s] = __builtin_bit_cast(h8, u4v{lo.x, lo.y, hi.x, hi.y});
+        }
       }
     }
     // the slots are reused only after these reads have completed
@@ -178,10 +252,8 @@ __device__ __forceinline__ void gemvq_body(const GvqArgs& a) {
         } else {
           gv3_wait_vm<0>();
         }
-        const uint8_t* wp = (const uint8_t*)ring + 1024 * NI * (t % R) + 16 * PR * j + my_off(t);
-        typename FmtTraits<FMT>::Frag f;
-        load_unit<FMT>(f, wp, g, 0);
-        acc[tt] = gvd_superblock<FMT>(f, xa, g);
+        const uint8_t* wp = (const uint8_t*)ring + SLOT * (t % R) + 16 * PR * j + my_off(t);
+        acc[tt] = gvq_column<FMT>(wp, xa, g);
         // this slot is refilled in a later iteration: its reads must be done
         __builtin_amdgcn_s_waitcnt(0xC07F);
         asm volatile("" ::: "memory");

@@ -238,7 +238,7 @@ struct DeviceModule {
   hipFunction_t gemv2[kNumFormats][2][2] = {};  // K-quants only     // [format][y f16]
   hipFunction_t gemvd[kNumFormats][3][2] = {};  // K-quants only: [format][NT 1, 2, 4][y f16]
   hipFunction_t gemvs[kNumFormats][2] = {};  // K-quants only: [format][y f16]
-  hipFunction_t gemvq[kNumFormats][2] = {};  // K-quants only: [format][y f16]
+  hipFunction_t gemvq[kNumFormats][2] = {};  // [format][y f16]
   hipFunction_t gemml[kNumFormats][2][2] = {};  // 32-value formats only: [format][NT - 1][y f16]
   hipFunction_t gemvr[2][4] = {};  // Q4_K rows split across lanes: [y f16][log2 activation pieces per thread]
   int cus = 0;                        // compute units of the device
@@ -384,16 +384,19 @@ void load_module(DeviceModule& d, int dev) {
         }
       }
   }
+  for (int fi = 0; fi < kNumFormats; fi++)
+    for (int yt = 0; yt < 2; yt++) {
+      snprintf(name, sizeof name, "cq_gemvq_%s_y%s", fmt_name(kFormats[fi]), yt ? "f16" : "f32");
+      if (get(&d.gemvq[fi][yt], name) != hipSuccess) {
+        d.err = std::string("missing kernel ") + name;
+        return;
+      }
+    }
   for (int fi = 0; fi < kNumFormats; fi++) {
     if (block_values(kFormats[fi]) != 256) continue;
     for (int yt = 0; yt < 2; yt++) {
       snprintf(name, sizeof name, "cq_gemvs_%s_y%s", fmt_name(kFormats[fi]), yt ? "f16" : "f32");
       if (get(&d.gemvs[fi][yt], name) != hipSuccess) {
-        d.err = std::string("missing kernel ") + name;
-        return;
-      }
-      snprintf(name, sizeof name, "cq_gemvq_%s_y%s", fmt_name(kFormats[fi]), yt ? "f16" : "f32");
-      if (get(&d.gemvq[fi][yt], name) != hipSuccess) {
         d.err = std::string("missing kernel ") + name;
         return;
       }
@@ -805,21 +808,24 @@ static cq_status launch_gemvs(DeviceModule* dm, const cq_weight* w, const void* 
 }
 
 // Batched decode with every activation fragment loaded once per workgroup
-// (cq_gemvq_*, K-quants, 2 <= m <= 16): one wave per superblock column of a
-// slice of at most 16 columns (rows of more superblocks are cut into
-// ceil(units / 16) slices of equal length over blockIdx.y, and
+// (cq_gemvq_*, every format, fp16 x, 2 <= m <= 16, K a multiple of 256): one
+// wave per column of 256 values (a K-quant superblock, or 8 blocks of a
+// 32-value format) of a slice of at most 16 columns (longer rows are cut
+// into ceil(units / 16) slices of equal length over blockIdx.y, and
 // cq_splitk_reduce_* adds their fp32 partials in slice order), workgroups
 // over balanced ranges of 16-row tiles, at most as many workgroups as fit
 // on the compute units at once.  LDS per wave: 10 KB, a DMA ring of two
-// slots (3 KB for Q4_K / Q5_K, 4 KB for Q6_K), which also carries the
-// activation transit, and the rest for the partial sums of 1 KB per tile of
-// a reduction chunk.  Needs the weight, its size and the activations
-// 16-byte aligned (whole 16-byte DMA pieces).  The slices' partials come
-// from the device's kept scratch (with_kept_scratch), or, while capturing
-// and in cq_matmul_noalloc, from its fixed buffer; when that is not to be
-// had (*declined set, nothing launched) the caller takes cq_gemvd_*.
+// slots of 16 rows x one column (2.25 KB for Q4_K / Q4_0 up to 4.25 KB for
+// Q8_0), which also carries the activation transit, and the rest for the
+// partial sums of 1 KB per tile of a reduction chunk.  Needs the weight,
+// its size and the activations 16-byte aligned (whole 16-byte DMA pieces).
+// The slices' partials come from the device's kept scratch
+// (with_kept_scratch), or, while capturing and in cq_matmul_noalloc, from
+// its fixed buffer; when that is not to be had (*declined set, nothing
+// launched) the caller takes the next kernel.
 static bool gemvq_fits(const cq_weight* w, const void* x) {
-  return gemvs_fits(w) && w->k / 256 <= 128 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+  return w->k % 256 == 0 && w->k / 256 <= 128 && (reinterpret_cast<uintptr_t>(w->dev) & 15) == 0 &&
+         w->nbytes % 16 == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
 }
 static int gemvq_lds_bytes(int nw) { return nw * 10 * 1024; }
 static cq_status launch_gemvq(DeviceModule* dm, const cq_weight* w, const void* x, int64_t m, void* y, int yt,
@@ -1340,7 +1346,7 @@ static cq_status matmul_impl(const cq_weight* w, const void* x, int x_dtype, int
     if (gemv1k_fits(w) && knobs().gemv1k) return launch_gemv1k(dm, w, x, y, yt, (hipStream_t)stream, epi);
     if (kq && w->k / 256 <= 64 && gemv2_fits(w)) return launch_gemv2(dm, w, x, y, yt, (hipStream_t)stream, epi);
   }
-  if (kq && !xt && m >= 2 && m <= 16 && knobs().gemvq && gemvq_fits(w, x) &&
+  if (!xt && m >= 2 && m <= 16 && knobs().gemvq && gemvq_fits(w, x) &&
       (w->k / 256 <= 16 || knobs().gemvq == 2 || knobs().gemvq_long)) {
     bool declined;
     const cq_status st = launch_gemvq(dm, w, x, m, y, yt, (hipStream_t)stream, epi, &declined);

@@ -35,3 +35,13 @@ GEMVQ_KERNEL(cq_gemvq_q5_k_yf32, CQ_Q5_K, 0)
 GEMVQ_KERNEL(cq_gemvq_q5_k_yf16, CQ_Q5_K, 1)
 GEMVQ_KERNEL(cq_gemvq_q6_k_yf32, CQ_Q6_K, 0)
 GEMVQ_KERNEL(cq_gemvq_q6_k_yf16, CQ_Q6_K, 1)
+GEMVQ_KERNEL(cq_gemvq_q4_0_yf32, CQ_Q4_0, 0)
+GEMVQ_KERNEL(cq_gemvq_q4_0_yf16, CQ_Q4_0, 1)
+GEMVQ_KERNEL(cq_gemvq_q5_0_yf32, CQ_Q5_0, 0)
+GEMVQ_KERNEL(cq_gemvq_q5_0_yf16, CQ_Q5_0, 1)
+GEMVQ_KERNEL(cq_gemvq_q8_0_yf32, CQ_Q8_0, 0)
+GEMVQ_KERNEL(cq_gemvq_q8_0_yf16, CQ_Q8_0, 1)
+GEMVQ_KERNEL(cq_gemvq_q4_1_yf32, CQ_Q4_1, 0)
+GEMVQ_KERNEL(cq_gemvq_q4_1_yf16, CQ_Q4_1, 1)
+GEMVQ_KERNEL(cq_gemvq_q5_1_yf32, CQ_Q5_1, 0)
+GEMVQ_KERNEL(cq_gemvq_q5_1_yf16, CQ_Q5_1, 1)

@@ -396,7 +396,8 @@ def test_graph_capture_prefill_split(cuda, fmt, n, k, m):
 
 
 @pytest.mark.parametrize("fmt,n,k,m", [(QuantFormat.Q4K, 4096, 14336, 16), (QuantFormat.Q6K, 300, 18944, 5),
-                                        (QuantFormat.Q5K, 1000, 8192, 9)])
+                                        (QuantFormat.Q5K, 1000, 8192, 9), (QuantFormat.Q8_0, 700, 14336, 12),
+                                        (QuantFormat.Q4_1, 300, 8192, 3)])
 def test_graph_capture_batched_slices(cuda, fmt, n, k, m):
     """Batched decode of rows longer than 16 superblocks captured into a HIP
     graph: the captured column kernel takes its slice partials from the
@@ -504,15 +505,16 @@ def test_gemv_batched_direct(cuda, monkeypatch, fmt, nt, nw, n, k, m):
     assert np.array_equal(a.view(np.uint32), _run(w, x, torch.float16, torch.float32).view(np.uint32))
 
 
-@pytest.mark.parametrize("fmt", KQ)
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("groups", ["0", "1", "3", "7"])
 @pytest.mark.parametrize("n,k,m", [(300, 4096, 2), (35, 512, 16), (97, 3584, 7), (33, 256, 16), (500, 1792, 9),
                                    (1000, 2048, 16), (129, 3840, 3), (4100, 4096, 13), (70, 1280, 15),
                                    (70, 14336, 4), (300, 18944, 9), (33, 4352, 16), (129, 8192, 3)])
 def test_gemv_batched_columns(cuda, monkeypatch, fmt, groups, n, k, m):
     """Batched decode (2 <= m <= 16, fp16 x) through the column kernel
-    (cq_gemvq_*): one wave per superblock column (1 to 16), rows of more
-    than 16 superblocks cut into slices (4 x 14, 5 x 15 with an idle wave in
+    (cq_gemvq_*), every format: one wave per column of 256 values (a
+    superblock, or 8 blocks of a 32-value format; 1 to 16 columns), rows of
+    more than 16 columns cut into slices (4 x 14, 5 x 15 with an idle wave in
     the last, 2 x 9 with one idle, 2 x 16) whose partials are summed in
     order, ragged last tile, tile ranges split over the default grid or 1, 3 or 7
     workgroups (runs of many tiles: the two-slot ring wraps, reduction
@@ -521,7 +523,8 @@ def test_gemv_batched_columns(cuda, monkeypatch, fmt, groups, n, k, m):
     byte offset of their 16-byte pieces (odd superblock counts); fp32 and
     fp16 y and the bias epilogue, against the oracle and bit-for-bit stable
     over repeated launches.  A weight whose size is not a multiple of 16
-    bytes takes cq_gemvd_* (the DMA reads whole pieces)."""
+    bytes takes the next kernel (the DMA reads whole pieces): cq_gemvd_* for
+    the K-quants, the 16-row MFMA GEMV for the others."""
     import torch
     monkeypatch.setenv("COMBS_GEMVQ_GROUPS", groups)
     data = synth(fmt, n, k)
@@ -536,9 +539,10 @@ def test_gemv_batched_columns(cuda, monkeypatch, fmt, groups, n, k, m):
     xd = torch.from_numpy(x).cuda().half()
     kern = L.path_name(w, xd, torch.empty((m, n), device="cuda"))
     print(f"gemvq {fmt.name} groups={groups} n={n} k={k} m={m} kernels={kern}", flush=True)
-    assert kern.startswith("cq_gemvq_" if len(data) % 16 == 0 else "cq_gemvd_")
+    fallback = "cq_gemvd_" if fmt in KQ else "cq_gemv_"
+    assert kern.startswith("cq_gemvq_" if len(data) % 16 == 0 else fallback)
     a = _run(w, x, torch.float16, torch.float32)
-    O.assert_close(a, expect, 1e-3, "y32")
+    O.assert_close(a, expect, rel_of(fmt) if k <= 4096 else 1e-3, "y32")
     O.assert_close(_run(w, x, torch.float16, torch.float16), expect, 1e-3, "y16")
     assert np.array_equal(a.view(np.uint32), _run(w, x, torch.float16, torch.float32).view(np.uint32))
     b = np.linspace(-1, 1, n).astype(np.float32)

@@ -140,7 +140,7 @@ def test_gemvd_row_tiles_bit_identical(cuda, monkeypatch, fmt, nw):
         assert np.array_equal(v, outs["1"]), f"NT={nt} differs from NT=1"
 
 
-@pytest.mark.parametrize("fmt", KQ)
+@pytest.mark.parametrize("fmt", ALL)
 @pytest.mark.parametrize("m", [3, 16])
 def test_gemvq_groups_bit_identical(cuda, monkeypatch, fmt, m):
     """Batched decode through the column kernel: 1, 5, 64 workgroups and the
@@ -158,8 +158,8 @@ def test_gemvq_groups_bit_identical(cuda, monkeypatch, fmt, m):
         torch.cuda.synchronize()
         outs[gr] = _bits(y)
     wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
-    O.assert_close(outs["0"].view(np.float32), _x(m, k, 11).astype(np.float64) @ wd.T.astype(np.float64), 1e-3,
-                   "gemvq")
+    O.assert_close(outs["0"].view(np.float32), _x(m, k, 11).astype(np.float64) @ wd.T.astype(np.float64),
+                   1e-3, "gemvq")
     for gr, v in outs.items():
         assert np.array_equal(v, outs["0"]), f"{gr} workgroups differ from the default grid"
 

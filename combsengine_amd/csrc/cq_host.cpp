@@ -231,6 +231,7 @@ struct DeviceModule {
   hipFunction_t gemm2[kNumFormats][2][2][2] = {};  // [format][NT-1][MT/8-1][y f16], fp16 x
   hipFunction_t xsums = nullptr;
   hipFunction_t reduce[2] = {};       // split-K epilogue [y f16]
+  hipFunction_t split_f32 = nullptr;  // fp32 activations -> fp16 hi and lo rows
   hipFunction_t gemv1[kNumFormats][2][3] = {};  // [format][y f16][epilogue: none, general, gated]
   hipFunction_t gemv1_multi[kNumFormats][2] = {};  // several weights, one row: [format][y f16]
   hipFunction_t gemv1_i8[kNumFormats][2][2] = {};
@@ -242,7 +243,8 @@ struct DeviceModule {
   hipFunction_t gemml[kNumFormats][2][2] = {};  // 32-value formats only: [format][NT - 1][y f16]
   hipFunction_t gemvr[2][4] = {};  // Q4_K rows split across lanes: [y f16][log2 activation pieces per thread]
   int cus = 0;                        // compute units of the device
-  // Scratch kept across calls (batched decode slice partials): grown on
+  // Scratch kept across calls: [0] batched decode slice partials, [1] the
+  // fp32-activation split (whose inner call may take [0]).  Grown on
   // demand, never freed before the process ends; `ev` is recorded on the
   // stream of each use, and a call on another stream waits for it first.
   struct {
@@ -252,7 +254,7 @@ struct DeviceModule {
     hipEvent_t ev = nullptr;
     hipStream_t last = nullptr;
     bool used = false;
-  } kept;
+  } kept[2];
 };
 DeviceModule g_dev[kMaxDevices];
 
@@ -283,7 +285,8 @@ void load_module(DeviceModule& d, int dev) {
   auto get = [&d](hipFunction_t* f, const char* nm) {
     const std::string n(nm);
     const int mi = (n.rfind("cq_gemv1", 0) == 0 || n.rfind("cq_gemvr", 0) == 0) ? 1 : (n.rfind("cq_gemv2", 0) == 0 || n.rfind("cq_gemvq", 0) == 0) ? 2
-                   : (n.rfind("cq_gemm", 0) == 0 || n.rfind("cq_xsums", 0) == 0 || n.rfind("cq_splitk", 0) == 0) ? 3
+                   : (n.rfind("cq_gemm", 0) == 0 || n.rfind("cq_xsums", 0) == 0 || n.rfind("cq_splitk", 0) == 0 ||
+                      n.rfind("cq_split_f32", 0) == 0) ? 3
                    : 0;
     const hipError_t e = hipModuleGetFunction(f, d.mods[mi], nm);
     if (e == hipSuccess) d.names[*f] = nm;
@@ -410,6 +413,10 @@ void load_module(DeviceModule& d, int dev) {
         return;
       }
     }
+  if (get(&d.split_f32, "cq_split_f32") != hipSuccess) {
+    d.err = "missing kernel cq_split_f32";
+    return;
+  }
   if (get(&d.reduce[0], "cq_splitk_reduce_yf32") != hipSuccess ||
       get(&d.reduce[1], "cq_splitk_reduce_yf16") != hipSuccess) {
     d.err = "missing kernel cq_splitk_reduce_*";
@@ -442,8 +449,8 @@ cq_status device_module(DeviceModule** out) {
 // device time).  Not for use while capturing (the event record and wait
 // would become graph nodes).
 template <typename F>
-static hipError_t with_kept_scratch(DeviceModule* dm, hipStream_t s, size_t bytes, F enqueue) {
-  auto& k = dm->kept;
+static hipError_t with_kept_scratch(DeviceModule* dm, int slot, hipStream_t s, size_t bytes, F enqueue) {
+  auto& k = dm->kept[slot];
   std::lock_guard<std::mutex> lock(k.mu);
   hipError_t e;
   if (!k.ev && (e = hipEventCreateWithFlags(&k.ev, hipEventDisableTiming)) != hipSuccess) return e;
@@ -470,7 +477,7 @@ constexpr int kUnset = -1000000;
 struct Knobs {
   int gemv_waves, gemv1, gemv1k, gemv1_grid, gemv1_i8, gemv1_prefetch2, gemv1_span, gemv1_spread,
       gemv1_wave_major, gemv2, gemv2_wpc, gemvd, gvd_nt, gvd_waves, gemm_kernel, gemm_waves, gemm2_mt,
-      gemm2_nt, gemm2_split, gateup_fused, gemvr, gemvs, gemvs_split, gemvq, gemvq_groups, gemvq_long, gemml, gemml_nt,
+      gemm2_nt, gemm2_split, gateup_fused, gemvr, gemvs, gemvs_split, gemvq, gemvq_groups, gemvq_long, f32_split, gemml, gemml_nt,
       multi_fused;
 };
 Knobs g_knobs;
@@ -508,6 +515,7 @@ void read_knobs() {
   k.gemvq = env_int("COMBS_GEMVQ", 1);
   k.gemvq_groups = env_int("COMBS_GEMVQ_GROUPS", 0);
   k.gemvq_long = env_int("COMBS_GEMVQ_LONG", 1);
+  k.f32_split = env_int("COMBS_F32_SPLIT", 1);
   k.gemml = env_int("COMBS_GEMML", 1);
   k.gemml_nt = env_int("COMBS_GEMML_NT", 0);
   k.multi_fused = env_int("COMBS_MULTI_FUSED", 1);
@@ -890,7 +898,7 @@ static cq_status launch_gemvq(DeviceModule* dm, const cq_weight* w, const void* 
   if (!part_bytes) e = launch_all(nullptr);
   else if (fixed) e = launch_all(fixed->ptr);
   else if (g_plan) e = launch_all(nullptr);
-  else e = with_kept_scratch(dm, s, part_bytes, launch_all);
+  else e = with_kept_scratch(dm, 0, s, part_bytes, launch_all);
   if (e != hipSuccess) return fail(CQ_ERR_HIP, "batched decode launch: %s", hipGetErrorString(e));
   return CQ_OK;
 }
@@ -1311,6 +1319,68 @@ static cq_status launch_gemm(DeviceModule* dm, const cq_weight* w, const void* x
 
 // Shared by cq_matmul_path, cq_matmul_bias and cq_matmul_gate_up.
 static cq_status matmul_impl(const cq_weight* w, const void* x, int x_dtype, int64_t m, void* y, int y_dtype, int path,
+                             void* stream, const CqEpi& epi);
+
+// fp32 activations (m >= 2; the K-quants from m = 4, where it measured
+// faster), every format: x is split exactly as the fp32-x kernels split it
+// (hi = fp16(x), lo = fp16(x - hi)) into fp16 hi rows followed by lo rows
+// (cq_split_f32), which the fp16 kernels multiply in one pass over the
+// weight into fp32 [2][rows][n]; cq_splitk_reduce_* adds the halves and
+// applies the epilogue.  Up to m = 16 the rows go in blocks of at most 8,
+// so that each block's 16 fp16 rows take the batched column kernel;
+// above, all 2m rows go to the prefill GEMMs at once.  Scratch (2 rows x
+// (2k + 4n) bytes per row) from the device's kept scratch; while
+// capturing, in cq_matmul_noalloc and when 2m fp16 rows would exceed 2 GiB,
+// *declined is set (nothing launched) and the fp32-x kernels run instead.
+static cq_status matmul_f32_split(DeviceModule* dm, const cq_weight* w, const void* x, int64_t m, void* y, int yt,
+                                  int path, hipStream_t s, const CqEpi& epi, bool* declined) {
+  *declined = true;
+  if (g_fixed) return CQ_OK;
+  if (!g_plan) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    HIP_TRY(hipStreamIsCapturing(s, &cs));
+    if (cs != hipStreamCaptureStatusNone) return CQ_OK;
+  }
+  if ((uint64_t)(2 * m) * (uint64_t)w->k * 2u >= (1ull << 31)) return CQ_OK;
+  *declined = false;
+  const int64_t mb = m <= 16 ? std::min<int64_t>(m, 8) : m;  // rows per block
+  const size_t xh_bytes = ((size_t)(2 * mb) * w->k * 2 + 255) & ~(size_t)255;
+  const size_t yb_bytes = (size_t)(2 * mb) * w->n * 4;
+  const size_t ysz = yt ? 2 : 4;
+  const size_t asz = epi.aux_f16 ? 2 : 4;
+  cq_status inner = CQ_OK;
+  auto run = [&](void* ws) -> hipError_t {
+    void* xh = ws;  // fp16 [2][rows][k]
+    float* yb = (float*)((char*)ws + xh_bytes);
+    for (int64_t r0 = 0; r0 < m; r0 += mb) {
+      const int64_t rows = std::min(mb, m - r0);
+      const void* xb = (const float*)x + r0 * w->k;
+      void* yo = (char*)y + (size_t)r0 * w->n * ysz;
+      CqEpi ep = epi;
+      if (ep.aux) ep.aux = (const char*)ep.aux + (size_t)r0 * w->n * asz;
+      long long mk = rows * w->k;
+      void* sp[] = {&xb, &xh, &mk};
+      hipError_t e = klaunch(dm, dm->split_f32, (unsigned)((mk + 1023) / 1024), 1, 1, 256, 0, s, sp);
+      if (e != hipSuccess) return e;
+      inner = matmul_impl(w, xh, CQ_F16, 2 * rows, yb, CQ_F32, path, s, CqEpi{});
+      if (inner != CQ_OK) return hipErrorLaunchFailure;
+      long long mn = rows * w->n;
+      int n = (int)w->n, two = 2;
+      void* rp[] = {&yb, &yo, &two, &mn, &n, &ep};
+      e = klaunch(dm, dm->reduce[yt], (unsigned)((mn + 255) / 256), 1, 1, 256, 0, s, rp);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  };
+  // a dry run needs only aligned stand-in addresses
+  const hipError_t e = g_plan ? run(reinterpret_cast<void*>(static_cast<uintptr_t>(256)))
+                              : with_kept_scratch(dm, 1, s, xh_bytes + yb_bytes, run);
+  if (inner != CQ_OK) return inner;
+  if (e != hipSuccess) return fail(CQ_ERR_HIP, "fp32 activation split: %s", hipGetErrorString(e));
+  return CQ_OK;
+}
+
+static cq_status matmul_impl(const cq_weight* w, const void* x, int x_dtype, int64_t m, void* y, int y_dtype, int path,
                              void* stream, const CqEpi& epi) {
   if (!w || !x || !y) return fail(CQ_ERR_NULL, "NULL weight, x or y");
   if (x_dtype != CQ_F16 && x_dtype != CQ_F32) return fail(CQ_ERR_BAD_DTYPE, "x_dtype %d", x_dtype);
@@ -1323,6 +1393,11 @@ static cq_status matmul_impl(const cq_weight* w, const void* x, int x_dtype, int
   cq_status st = device_module(&dm);
   if (st != CQ_OK) return st;
   const int xt = x_dtype == CQ_F32, yt = y_dtype == CQ_F16;
+  if (xt && knobs().f32_split && (m >= 4 || (m >= 2 && block_values(w->format) != 256) || knobs().f32_split == 2)) {
+    bool declined;
+    st = matmul_f32_split(dm, w, x, m, y, yt, path, (hipStream_t)stream, epi, &declined);
+    if (!declined) return st;
+  }
   // Prefill GEMM for m > 16 (or when forced): cq_gemm2_* / cq_gemm_* for the
   // K-quants, cq_gemml_* for the 32-value formats with fp16 x; the GEMV
   // kernels tile m by 16 otherwise.

@@ -67,6 +67,23 @@ extern "C" __global__ void __launch_bounds__(256) cq_xsums_f16(const _Float16* x
   xsums_body(x, xs, M, K);
 }
 
+// fp32 activations as two fp16 row blocks: xh[i] = hi = fp16(x[i]) and
+// xh[mk + i] = lo = fp16(x[i] - hi) (the hi + lo pair the fp32-x kernels
+// also use); four values per thread.
+extern "C" __global__ void __launch_bounds__(256) cq_split_f32(const float* x, _Float16* xh, long long mk) {
+  const long long i0 = 4 * ((long long)blockIdx.x * blockDim.x + threadIdx.x);
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const long long i = i0 + e;
+    if (i < mk) {
+      const float v = x[i];
+      const _Float16 hi = (_Float16)v;
+      xh[i] = hi;
+      xh[mk + i] = (_Float16)(v - (float)hi);
+    }
+  }
+}
+
 // Prefill dequant-GEMM for the 32-value block formats (cq_gemml.h):
 // [format] x [NT 1, 2] x [y dtype]; two workgroups per compute unit.
 #define GEMML_KERNEL(NAME, FMT, YT, NT)                                                                     \

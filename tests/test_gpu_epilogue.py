@@ -31,7 +31,7 @@ def _x(m, k, seed):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("m", [1, 4, 64])
+@pytest.mark.parametrize("m", [1, 4, 12, 64])
 @pytest.mark.parametrize("bias_dt", ["f32", "f16"])
 @pytest.mark.parametrize("y_dt", ["f32", "f16"])
 def test_bias_epilogue(cuda, fmt, m, bias_dt, y_dt):
@@ -92,7 +92,7 @@ PAIRS = [(QuantFormat.Q4K, QuantFormat.Q4K), (QuantFormat.Q4K, QuantFormat.Q6K),
 
 @pytest.mark.parametrize("gf,uf", PAIRS)
 @pytest.mark.parametrize("act", [Activation.Silu, Activation.GeluTanh, Activation.Gelu])
-@pytest.mark.parametrize("m", [1, 4, 64, 130])
+@pytest.mark.parametrize("m", [1, 4, 12, 64, 130])
 @pytest.mark.parametrize("y_dt", ["f32", "f16"])
 def test_gate_up_epilogue(cuda, gf, uf, act, m, y_dt):
     """y = act(x.G^T) * (x.U^T).  With an fp16 output the library rounds the

@@ -551,6 +551,36 @@ def test_gemv_batched_columns(cuda, monkeypatch, fmt, groups, n, k, m):
     O.assert_close(yb.cpu().numpy(), expect.astype(np.float64) + b, 1e-3, "bias")
 
 
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("n,k", [(300, 4096), (97, 1536), (70, 14336)])
+@pytest.mark.parametrize("m", [2, 4, 9, 16, 17, 40])
+def test_f32_activations_split(cuda, monkeypatch, fmt, n, k, m):
+    """fp32 activations at m >= 2 through the split path (x = hi + lo fp16
+    rows, one pass of the fp16 kernels over 2m rows, the halves added by the
+    split-K reduction; rows in blocks of 8 up to m = 16): against float64 of
+    the oracle's dequant at the fp32-x bar, against the fp32-x kernels
+    (COMBS_F32_SPLIT=0) and bit-for-bit stable over repeats; the dry run
+    names the split kernels where the split is taken (K-quants from m = 4,
+    the 32-value formats from m = 2)."""
+    import torch
+    data = synth(fmt, n, k)
+    wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
+    w = QuantWeight.from_gguf_bytes(fmt, data, n, k)
+    rng = np.random.default_rng(90 + m)
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    expect = x.astype(np.float64) @ wd.astype(np.float64).T
+    kern = L.kernels(w, L.CQ_F32, m, L.CQ_F32)
+    print(f"f32 split {fmt.name} [{n}x{k}] m={m} kernels={kern}", flush=True)
+    assert kern.startswith("cq_split_f32") == (m >= 4 or fmt not in KQ), kern
+    a = _run(w, x, torch.float32, torch.float32)
+    O.assert_close(a, expect, rel_of(fmt), "split")
+    assert np.array_equal(a.view(np.uint32), _run(w, x, torch.float32, torch.float32).view(np.uint32))
+    O.assert_close(_run(w, x, torch.float32, torch.float16), expect, 1e-3, "split y16")
+    monkeypatch.setenv("COMBS_F32_SPLIT", "0")
+    assert not L.kernels(w, L.CQ_F32, m, L.CQ_F32).startswith("cq_split_f32")
+    O.assert_close(a, _run(w, x, torch.float32, torch.float32), 2 * rel_of(fmt), "vs the fp32-x kernels")
+
+
 @pytest.mark.parametrize("fmt", KQ)
 @pytest.mark.parametrize("m", [4, 16])
 def test_gemv_batched_gaussian_column_shape(cuda, fmt, m):

@@ -103,12 +103,16 @@ const void* cq_weight_device_ptr(const cq_weight* w);
  * QuantLinearOp::forward it serves (qlinear.rs:58).  x: device, x_dtype
  * CQ_F16 or CQ_F32; y: device, caller-allocated, y_dtype CQ_F32 or CQ_F16.
  * fp32 activations must be finite and below 65504 in magnitude (they are fed
- * to the fp16 matrix cores as a hi+lo pair).  Prefill (m > 16) and
- * batched decode (2 <= m <= 16) of rows longer than 16 superblocks take
- * stream-ordered scratch (activation sums, split partials); while the
- * stream is being captured into a HIP graph they take the device's fixed
- * array instead (see cq_matmul_noalloc), which graphs captured this way
- * share: replays that overlap on one device race. */
+ * to the fp16 matrix cores as a hi+lo pair; at m >= 2 -- m >= 4 for the
+ * K-quants -- that split is made once into 2m fp16 rows that the fp16
+ * kernels multiply in one pass).  Prefill (m > 16) takes stream-ordered
+ * scratch (activation sums, split partials); batched decode (2 <= m <= 16)
+ * of rows longer than 4096 values and the fp32 split take a per-device
+ * buffer kept across calls (ordered across streams by an event).  While
+ * the stream is being captured into a HIP graph, prefill and batched
+ * decode take the device's fixed array instead (see cq_matmul_noalloc),
+ * which graphs captured this way share: replays that overlap on one device
+ * race; captured fp32 activations run the fp32-x kernels. */
 cq_status cq_matmul(const cq_weight* w, const void* x, int x_dtype, int64_t m, void* y, int y_dtype,
                     void* stream);
 

@@ -16,7 +16,11 @@
 //   - a block's MFMA starts from zero and its fp32 result is scaled by the
 //     block's fp16 d into the accumulator (every 32 K values carry their own
 //     scale, so nothing can be folded into the operands exactly); Q4_1 /
-//     Q5_1 add m * sum(x of the block), the sum by one more MFMA against B = 1.
+//     Q5_1 add m * sum(x of the block), the sum by one more MFMA against B = 1
+//     (once per activation tile, shared by the NT weight tiles);
+//   - when the tile grid leaves compute units idle (few weight rows or
+//     activation rows), the steps are split over blockIdx.z; each slice
+//     writes fp32 partials and cq_splitk_reduce_* sums them in slice order.
 #pragma once
 #include <type_traits>
 #include "cq_gemm2.h"
@@ -24,9 +28,11 @@
 struct LgArgs {
   const uint8_t* w;    // packed blocks, [N rows][row_bytes]
   const _Float16* x;   // [M][K]
-  void* y;             // [M][N] fp32 or fp16
+  void* y;             // [M][N] fp32 or fp16 (no split)
+  float* part;         // split: [slices][M][N] fp32 partial sums, else null
   long long row_bytes;
   int M, N, K, blocks; // blocks = K / 32
+  int ssteps;          // steps (4 blocks) per slice (blockIdx.z)
   CqEpi epi;
 };
 
@@ -66,6 +72,7 @@ __device__ __forceinline__ void gemml_body(const LgArgs& a) {
   // v ^ (r & 15).  Rows >= M re-read row M - 1, chunks past K re-read the
   // row's last chunk (neither is used).
   const int steps = (a.blocks + LB - 1) / LB;
+  const int st0 = (int)blockIdx.z * a.ssteps, st1 = min(steps, st0 + a.ssteps);  // this slice's steps
   auto dma_x = [&](_Float16* buf, int step) {
 #pragma unroll
     for (int ii = 0; ii < 4 * MT / NW; ii++) {
@@ -96,16 +103,16 @@ __device__ __forceinline__ void gemml_body(const LgArgs& a) {
       return (h8)__builtin_shufflevector(p, q, 0, 1, 2, 3, 4, 5, 6, 7);
     }
   };
-  dma_x(lg_x0, 0);
-  load_w(cur, 0);
+  dma_x(lg_x0, st0);
+  load_w(cur, st0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   const uint32_t ones = 0x3C003C00u;
   const h8 bones = mk_h8(ones, ones, ones, ones);
-  for (int step = 0; step < steps; step++) {
-    const _Float16* xc = (step & 1) ? lg_x1 : lg_x0;
-    _Float16* xn = (step & 1) ? lg_x0 : lg_x1;
-    const bool more = step + 1 < steps;
+  for (int step = st0; step < st1; step++) {
+    const _Float16* xc = ((step - st0) & 1) ? lg_x1 : lg_x0;
+    _Float16* xn = ((step - st0) & 1) ? lg_x0 : lg_x1;
+    const bool more = step + 1 < st1;
     if (more) {
       dma_x(xn, step + 1);
       load_w(nxt, step + 1);
@@ -126,13 +133,14 @@ __device__ __forceinline__ void gemml_body(const LgArgs& a) {
 #pragma unroll
       for (int tm = 0; tm < MT; tm++) {
         const h8 av = afrag(xc, tm, i);
+        f4 sx = {0, 0, 0, 0};
+        if constexpr (lg_affine<FMT>()) sx = mfma(av, bones, f4{0, 0, 0, 0});
 #pragma unroll
         for (int t = 0; t < NT; t++) {
           const f4 c = mfma(av, b[t], f4{0, 0, 0, 0});
 #pragma unroll
           for (int r = 0; r < 4; r++) acc[t][tm][r] = __builtin_fmaf(d[t], c[r], acc[t][tm][r]);
           if constexpr (lg_affine<FMT>()) {
-            const f4 sx = mfma(av, bones, f4{0, 0, 0, 0});
 #pragma unroll
             for (int r = 0; r < 4; r++) acc[t][tm][r] = __builtin_fmaf(mm[t], sx[r], acc[t][tm][r]);
           }
@@ -153,6 +161,9 @@ __device__ __forceinline__ void gemml_body(const LgArgs& a) {
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const int m = m0 + 16 * tm + 4 * g + r, n = n0 + 16 * t + j;
-        if (m < a.M && n < a.N) cq_store<YT>(a.y, a.epi, acc[t][tm][r], (size_t)m * a.N + n, n);
+        if (m < a.M && n < a.N) {
+          if (a.part) a.part[((size_t)blockIdx.z * a.M + m) * a.N + n] = acc[t][tm][r];
+          else cq_store<YT>(a.y, a.epi, acc[t][tm][r], (size_t)m * a.N + n, n);
+        }
       }
 }

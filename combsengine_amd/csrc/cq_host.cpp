@@ -207,8 +207,10 @@ struct LgArgs {
   const void* w;
   const void* x;
   void* y;
+  float* part;
   long long row_bytes;
   int M, N, K, blocks;
+  int ssteps;
   CqEpi epi;
 };
 struct DequantArgs {
@@ -477,7 +479,7 @@ constexpr int kUnset = -1000000;
 struct Knobs {
   int gemv_waves, gemv1, gemv1k, gemv1_grid, gemv1_i8, gemv1_prefetch2, gemv1_span, gemv1_spread,
       gemv1_wave_major, gemv2, gemv2_wpc, gemvd, gvd_nt, gvd_waves, gemm_kernel, gemm_waves, gemm2_mt,
-      gemm2_nt, gemm2_split, gateup_fused, gemvr, gemvs, gemvs_split, gemvq, gemvq_groups, gemvq_long, f32_split, gemml, gemml_nt,
+      gemm2_nt, gemm2_split, gateup_fused, gemvr, gemvs, gemvs_split, gemvq, gemvq_groups, gemvq_long, f32_split, gemml, gemml_nt, gemml_split,
       multi_fused;
 };
 Knobs g_knobs;
@@ -518,6 +520,7 @@ void read_knobs() {
   k.f32_split = env_int("COMBS_F32_SPLIT", 1);
   k.gemml = env_int("COMBS_GEMML", 1);
   k.gemml_nt = env_int("COMBS_GEMML_NT", 0);
+  k.gemml_split = env_int("COMBS_GEMML_SPLIT", 0);
   k.multi_fused = env_int("COMBS_MULTI_FUSED", 1);
   g_knobs = k;
 }
@@ -1275,6 +1278,7 @@ static cq_status launch_gemml(DeviceModule* dm, const cq_weight* w, const void* 
   a.w = w->dev;
   a.x = x;
   a.y = y;
+  a.part = nullptr;
   a.row_bytes = (long long)(w->nbytes / (size_t)w->n);
   a.M = (int)m;
   a.N = (int)w->n;
@@ -1286,8 +1290,49 @@ static cq_status launch_gemml(DeviceModule* dm, const cq_weight* w, const void* 
   if (nt != 1 && nt != 2) nt = ((w->n + 127) / 128) * mblk >= dm->cus ? 2 : 1;
   const long long gx = (w->n + 64 * nt - 1) / (64 * nt);
   if (gx > 0x7fffffffLL || mblk > 65535) return fail(CQ_ERR_BAD_SHAPE, "grid too large");
+  // K slices while the grid leaves compute units idle (two workgroups fit
+  // on one), each of at least 3 steps; COMBS_GEMML_SPLIT forces the count.
+  // Partials from the stream-ordered pool, or the fixed buffer while
+  // capturing and in cq_matmul_noalloc (the split halves until they fit).
+  const int steps = (a.blocks + 3) / 4;  // steps of four blocks (the kernel's LB)
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (!g_plan) HIP_TRY(hipStreamIsCapturing(s, &cs));
+  const FixedScratch* fixed = g_fixed;
+  FixedScratch cap_fs{nullptr, 0};
+  if (!fixed && cs != hipStreamCaptureStatusNone) {
+    if (cq_scratch_device_ptr(&cap_fs.ptr, &cap_fs.bytes) == hipSuccess) fixed = &cap_fs;
+    else (void)hipGetLastError();
+  }
+  int splits = (cs == hipStreamCaptureStatusNone || fixed) ? knobs().gemml_split : 1;
+  if (splits < 1) {
+    splits = 1;
+    while (gx * mblk * splits * 2 <= 2LL * dm->cus && steps / (splits * 2) >= 3) splits *= 2;
+  }
+  if (splits > steps) splits = steps;
+  auto part_size = [&](int sp) -> size_t { return sp > 1 ? (size_t)sp * m * w->n * 4 : 0; };
+  if (fixed)
+    while (splits > 1 && part_size(splits) > fixed->bytes) splits /= 2;
+  a.ssteps = (steps + splits - 1) / splits;
+  splits = (steps + a.ssteps - 1) / a.ssteps;
+  const size_t part_bytes = part_size(splits);
+  void* ws = nullptr;
+  if (part_bytes) {
+    if (fixed) ws = fixed->ptr;
+    else if (!g_plan) HIP_TRY(hipMallocAsync(&ws, part_bytes, s));
+    a.part = (float*)ws;
+  }
   void* params[] = {&a};
-  HIP_TRY(klaunch(dm, dm->gemml[fi][nt - 1][yt], (unsigned)gx, (unsigned)mblk, 1, 256, 0, s, params));
+  hipError_t e = klaunch(dm, dm->gemml[fi][nt - 1][yt], (unsigned)gx, (unsigned)mblk, (unsigned)splits, 256, 0, s,
+                         params);
+  if (e == hipSuccess && part_bytes) {
+    long long mn = m * w->n;
+    int n = (int)w->n;
+    CqEpi ep = epi;
+    void* rp[] = {&a.part, &y, &splits, &mn, &n, &ep};
+    e = klaunch(dm, dm->reduce[yt], (unsigned)((mn + 255) / 256), 1, 1, 256, 0, s, rp);
+  }
+  if (ws && !fixed) HIP_TRY(hipFreeAsync(ws, s));
+  if (e != hipSuccess) return fail(CQ_ERR_HIP, "legacy prefill launch: %s", hipGetErrorString(e));
   return CQ_OK;
 }
 

@@ -352,9 +352,11 @@ def test_graph_capture_replays(cuda, monkeypatch):
 
 
 @pytest.mark.parametrize("fmt,n,k,m", [(QuantFormat.Q6K, 512, 3584, 512), (QuantFormat.Q4K, 512, 3584, 130),
-                                        (QuantFormat.Q5K, 300, 4096, 40), (QuantFormat.Q4K, 1024, 4096, 256)])
+                                        (QuantFormat.Q5K, 300, 4096, 40), (QuantFormat.Q4K, 1024, 4096, 256),
+                                        (QuantFormat.Q8_0, 1024, 4096, 100), (QuantFormat.Q5_1, 512, 3584, 40)])
 def test_graph_capture_prefill_split(cuda, fmt, n, k, m):
-    """Prefill captured into a HIP graph with the default K split: the
+    """Prefill captured into a HIP graph with the default K split (the
+    K-quants' cq_gemm2_* and the 32-value formats' cq_gemml_*): the
     captured launch takes its activation sums and split partials from the
     device's fixed scratch buffer (no allocation in the graph) and must give
     the eager launch's bits (same kernels and slices, eager scratch allocated
@@ -713,14 +715,19 @@ def test_gemv_batched_shared(cuda, monkeypatch, fmt, split, n, k, m):
 
 @pytest.mark.parametrize("fmt", sorted(LEGACY))
 @pytest.mark.parametrize("nt", ["1", "2"])
+@pytest.mark.parametrize("split", ["0", "1", "3"])
 @pytest.mark.parametrize("n,k,m", [(300, 320, 17), (130, 4096, 64), (1000, 1056, 130), (70, 2048, 300)])
-def test_gemm_legacy_formats(cuda, monkeypatch, fmt, nt, n, k, m):
+def test_gemm_legacy_formats(cuda, monkeypatch, fmt, nt, split, n, k, m):
     """Prefill GEMM for the 32-value formats (cq_gemml_*): 128-row activation
     tiles (ragged m), 16-row weight tiles (ragged n), steps of four blocks
     with a partial last step (k = 320, 1056), one or two weight tiles per
-    wave; fp32 and fp16 y and the bias epilogue, against the oracle."""
+    wave, the steps split over the grid (automatic, one, three slices: the
+    last shorter, or holding only the partial step) with the slices'
+    partials summed by cq_splitk_reduce_*; fp32 and fp16 y and the bias
+    epilogue, against the oracle."""
     import torch
     monkeypatch.setenv("COMBS_GEMML_NT", nt)
+    monkeypatch.setenv("COMBS_GEMML_SPLIT", split)
     data = synth(fmt, n, k)
     wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
     w = QuantWeight.from_gguf_bytes(fmt, data, n, k)

@@ -46,17 +46,25 @@
 #include "cq_gemv1.h"
 
 #define GVQ_MAX_WAVES 16
+#define GVQ_MAX_SEG 4  // weights of one launch
 
+// Segments: the weights of one launch (same format and K, one activation
+// block): segment s owns global tiles [segt[s], segt[s + 1]) of 16 of its
+// rows.  Gated (two segments, gate and up of the same shape): every tile
+// is 8 gate rows and the same 8 up rows, and the output is act(gate) * up.
 struct GvqArgs {
-  const uint8_t* w;   // packed superblocks, [N rows][row_bytes]
   const _Float16* x;  // [M][K]
-  void* y;            // [M][N] fp32 or fp16 (no split)
-  float* part;        // split: [slices][M][N] fp32 partial sums, else null
+  float* part;        // split (one segment): [slices][M][N] fp32 partial sums, else null
   long long row_bytes;
-  long long wbytes;   // weight bytes (the DMA never reads past them)
-  int M, N, K, units;  // units = K / 256
-  int tiles;           // ceil(N / 16)
-  CqEpi epi;
+  int M, K, units;    // units = K / 256
+  int tiles;          // tiles of all segments
+  int nseg, gated;
+  int segt[GVQ_MAX_SEG + 1];
+  const uint8_t* segw[GVQ_MAX_SEG];  // packed weight, [N rows][row_bytes]
+  void* segy[GVQ_MAX_SEG];           // [M][N] fp32 or fp16
+  int segn[GVQ_MAX_SEG];             // N
+  long long segwb[GVQ_MAX_SEG];      // weight bytes (the DMA never reads past them)
+  CqEpi epi;          // one segment only (gated: epi.act)
 };
 
 // A column is 256 values of a row: one K-quant superblock, or 8 blocks of a
@@ -140,7 +148,8 @@ __device__ __forceinline__ f4 gvq_column(const uint8_t* wp, const h8 (&xa)[8], i
   }
 }
 
-template <int FMT, int YT>
+// MODE 0: one weight (segment 0); 1: segments; 2: gated pair.
+template <int FMT, int YT, int MODE>
 __device__ __forceinline__ void gemvq_body(const GvqArgs& a) {
   typedef GvqShape<FMT> S;
   constexpr int CB = S::CB, PR = S::PR, P = S::P, NI = S::NI, SLOT = S::SLOT, R = S::R, TC = S::TC;
@@ -176,21 +185,59 @@ __device__ __forceinline__ void gemvq_body(const GvqArgs& a) {
     poff[i] = 16 * (q - prow[i] * PR);
   }
   const size_t col = (size_t)(cb + wave) * CB;
-  const size_t wlast = (size_t)a.wbytes - 16;
+  // the segment holding global tile t (uniform), picked by a compare chain on
+  // t: a select on a segment index is folded back into a dynamic index into
+  // the kernel arguments, which the compiler then copies to scratch
+  struct Seg {
+    const uint8_t* w;
+    void* y;
+    size_t wlast;
+    int t0, n;
+  };
+  auto seg_at = [&](int t) {
+    Seg sg{a.segw[0], a.segy[0], (size_t)a.segwb[0] - 16, 0, a.segn[0]};
+    if constexpr (MODE == 1) {
+#pragma unroll
+      for (int k = 1; k < GVQ_MAX_SEG; k++)
+        if (k < a.nseg && t >= a.segt[k]) sg = Seg{a.segw[k], a.segy[k], (size_t)a.segwb[k] - 16, a.segt[k], a.segn[k]};
+    }
+    return sg;
+  };
+  // weight, and byte offset in it, of row r (0..15) of global tile t's
+  // column: gated tiles take rows 0-7 from the gate weight and 8-15 from the
+  // up weight, 8 rows of each per tile
+  auto row_src = [&](int t, int r, const uint8_t*& w, size_t& wlast) -> size_t {
+    const Seg sg = seg_at(t);
+    int row;
+    w = sg.w;
+    wlast = sg.wlast;
+    if constexpr (MODE == 2) {
+      row = 8 * t + (r & 7);
+      if (r >= 8) {
+        w = a.segw[1];
+        wlast = (size_t)a.segwb[1] - 16;
+      }
+    } else {
+      row = 16 * (t - sg.t0) + r;
+    }
+    return (size_t)min(row, sg.n - 1) * (size_t)a.row_bytes + col;
+  };
   auto dma = [&](int t) {  // tile t0 + t into slot t % R
-    const int n0 = 16 * (t0 + t);
     const uint32_t lb = rb + SLOT * (t % R);
 #pragma unroll
     for (int i = 0; i < NI; i++) {
-      const size_t s = (size_t)min(n0 + prow[i], a.N - 1) * (size_t)a.row_bytes + col;
+      const uint8_t* w;
+      size_t wlast;
+      const size_t s = row_src(t0 + t, prow[i], w, wlast);
       if (P % 64 == 0 || i + 1 < NI || 64 * i + lane < P)
-        gv3_dma16(a.w + min((s & ~(size_t)15) + poff[i], wlast), lb + 1024 * i);
+        gv3_dma16(w + min((s & ~(size_t)15) + poff[i], wlast), lb + 1024 * i);
     }
   };
-  // the lane's row within a slot: byte offset of its superblock
+  // the lane's row within a slot: byte offset of its column
   auto my_off = [&](int t) {
-    const size_t s = (size_t)min(16 * (t0 + t) + j, a.N - 1) * (size_t)a.row_bytes + col;
-    return (int)(s & 15);
+    const uint8_t* w;
+    size_t wlast;
+    return (int)(row_src(t0 + t, j, w, wlast) & 15);
   };
   // Activations of column `wave`, carried by the wave's LDS after slot 0
   // (slot 1 and the partial sums' space) in phases of PH row pairs while
@@ -277,10 +324,28 @@ __device__ __forceinline__ void gemvq_body(const GvqArgs& a) {
 #pragma unroll
         for (int w2 = 1; w2 < GVQ_MAX_WAVES; w2++)
           if (w2 < cols) s += v[w2];
-        const int m = 4 * (ln >> 4) + r, n = 16 * (t0 + c0 + tt) + (ln & 15);
-        if (m < a.M && n < a.N) {
-          if (a.part) a.part[((size_t)blockIdx.y * a.M + m) * a.N + n] = s;
-          else cq_store<YT>(a.y, a.epi, s, (size_t)m * a.N + n, n);
+        const int m = 4 * (ln >> 4) + r, t = t0 + c0 + tt, c = ln & 15;
+        if constexpr (MODE == 2) {
+          // columns c < 8: gate row 8 t + c; its up row is column c + 8
+          const int n = 8 * t + c, N = a.segn[0];
+          float u = 0.0f;
+          if (c < 8) {
+#pragma unroll
+            for (int w2 = 0; w2 < GVQ_MAX_WAVES; w2++) v[w2] = w2 < cols ? red_at(w2, tt, r, ln + 8) : 0.0f;
+            u = v[0];
+#pragma unroll
+            for (int w2 = 1; w2 < GVQ_MAX_WAVES; w2++)
+              if (w2 < cols) u += v[w2];
+          }
+          if (c < 8 && m < a.M && n < N) cq_store_raw<YT>(a.segy[0], cq_gated<YT>(s, u, a.epi.act), (size_t)m * N + n);
+        } else {
+          const Seg sg = seg_at(t);
+          const int n = 16 * (t - sg.t0) + c, N = sg.n;
+          void* const y = sg.y;
+          if (m < a.M && n < N) {
+            if (a.part) a.part[((size_t)blockIdx.y * a.M + m) * N + n] = s;
+            else cq_store<YT>(y, a.epi, s, (size_t)m * N + n, n);
+          }
         }
       }
     }

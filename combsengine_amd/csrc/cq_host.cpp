@@ -144,14 +144,19 @@ struct LtArgs {
   int M, N, K, units, usplit;
   CqEpi epi;
 };
+constexpr int kGvqMaxSeg = 4;
 struct GvqArgs {
-  const void* w;
   const void* x;
-  void* y;
   float* part;
   long long row_bytes;
-  long long wbytes;
-  int M, N, K, units, tiles;
+  int M, K, units;
+  int tiles;
+  int nseg, gated;
+  int segt[kGvqMaxSeg + 1];
+  const void* segw[kGvqMaxSeg];
+  void* segy[kGvqMaxSeg];
+  int segn[kGvqMaxSeg];
+  long long segwb[kGvqMaxSeg];
   CqEpi epi;
 };
 constexpr int kMultiMax = 4;  // weights per cq_matmul_multi launch (GV1_MSEG)
@@ -241,7 +246,7 @@ struct DeviceModule {
   hipFunction_t gemv2[kNumFormats][2][2] = {};  // K-quants only     // [format][y f16]
   hipFunction_t gemvd[kNumFormats][3][2] = {};  // K-quants only: [format][NT 1, 2, 4][y f16]
   hipFunction_t gemvs[kNumFormats][2] = {};  // K-quants only: [format][y f16]
-  hipFunction_t gemvq[kNumFormats][2] = {};  // [format][y f16]
+  hipFunction_t gemvq[kNumFormats][3][2] = {};  // [format][one weight, several, gated pair][y f16]
   hipFunction_t gemml[kNumFormats][2][2] = {};  // 32-value formats only: [format][NT - 1][y f16]
   hipFunction_t gemvr[2][4] = {};  // Q4_K rows split across lanes: [y f16][log2 activation pieces per thread]
   int cus = 0;                        // compute units of the device
@@ -391,10 +396,13 @@ void load_module(DeviceModule& d, int dev) {
   }
   for (int fi = 0; fi < kNumFormats; fi++)
     for (int yt = 0; yt < 2; yt++) {
-      snprintf(name, sizeof name, "cq_gemvq_%s_y%s", fmt_name(kFormats[fi]), yt ? "f16" : "f32");
-      if (get(&d.gemvq[fi][yt], name) != hipSuccess) {
-        d.err = std::string("missing kernel ") + name;
-        return;
+      for (int md = 0; md < 3; md++) {
+        snprintf(name, sizeof name, "cq_gemvq_%s%s_y%s", fmt_name(kFormats[fi]),
+                 md == 0 ? "" : md == 1 ? "_multi" : "_gated", yt ? "f16" : "f32");
+        if (get(&d.gemvq[fi][md][yt], name) != hipSuccess) {
+          d.err = std::string("missing kernel ") + name;
+          return;
+        }
       }
     }
   for (int fi = 0; fi < kNumFormats; fi++) {
@@ -840,25 +848,36 @@ static bool gemvq_fits(const cq_weight* w, const void* x) {
 }
 static int gemvq_lds_bytes(int nw) { return nw * 10 * 1024; }
 static cq_status launch_gemvq(DeviceModule* dm, const cq_weight* w, const void* x, int64_t m, void* y, int yt,
-                              hipStream_t s, const CqEpi& epi, bool* declined) {
+                              hipStream_t s, const CqEpi& epi, bool* declined, int nseg = 1,
+                              const cq_weight* const* ws = nullptr, void* const* ys = nullptr, bool gated = false) {
   *declined = false;
   const int fi = fmt_index(w->format);
   GvqArgs a{};
-  a.w = w->dev;
   a.x = x;
-  a.y = y;
   a.part = nullptr;
   a.row_bytes = (long long)(w->nbytes / (size_t)w->n);
-  a.wbytes = (long long)w->nbytes;
   a.M = (int)m;
-  a.N = (int)w->n;
   a.K = (int)w->k;
   a.units = (int)(w->k / 256);
   a.epi = epi;
-  const long long tiles = (w->n + 15) / 16;
+  a.nseg = nseg;
+  a.gated = gated ? 1 : 0;
+  long long tiles = 0;
+  for (int i = 0; i < nseg; i++) {
+    const cq_weight* wi = ws ? ws[i] : w;
+    a.segt[i] = (int)tiles;
+    a.segw[i] = wi->dev;
+    a.segy[i] = ys ? ys[i] : y;
+    a.segn[i] = (int)wi->n;
+    a.segwb[i] = (long long)wi->nbytes;
+    if (!gated) tiles += (wi->n + 15) / 16;
+  }
+  if (gated) tiles = (w->n + 7) / 8;  // 8 gate and 8 up rows per tile
   if (tiles > 0x7fffffffLL) return fail(CQ_ERR_BAD_SHAPE, "grid too large (n=%lld)", (long long)w->n);
+  a.segt[nseg] = (int)tiles;
   a.tiles = (int)tiles;
   const int slices = (a.units + 15) / 16;
+  if (slices > 1 && (nseg > 1 || gated)) return fail(CQ_ERR_BAD_SHAPE, "multi-weight batched decode: k > 4096");
   const int nw = (a.units + slices - 1) / slices;  // columns (waves) per slice
   const int lds = gemvq_lds_bytes(nw);
   const int per_cu = std::max(1, std::min(160 * 1024 / lds, 16 / nw));
@@ -884,11 +903,11 @@ static cq_status launch_gemvq(DeviceModule* dm, const cq_weight* w, const void* 
     *declined = true;
     return CQ_OK;
   }
-  auto launch_all = [&](void* ws) -> hipError_t {
-    a.part = (float*)ws;
+  auto launch_all = [&](void* ws_) -> hipError_t {
+    a.part = (float*)ws_;
     void* params[] = {&a};
-    hipError_t e = klaunch(dm, dm->gemvq[fi][yt], (unsigned)groups, (unsigned)slices, 1, 64 * nw, (unsigned)lds, s,
-                           params);
+    hipError_t e = klaunch(dm, dm->gemvq[fi][gated ? 2 : nseg > 1 ? 1 : 0][yt], (unsigned)groups, (unsigned)slices, 1,
+                           64 * nw, (unsigned)lds, s, params);
     if (e != hipSuccess || !part_bytes) return e;
     long long mn = m * w->n;
     int n = (int)w->n;
@@ -1526,6 +1545,22 @@ cq_status cq_matmul_gate_up(const cq_weight* gate, const cq_weight* up, const vo
     epi.act = act;
     return launch_gemv1(dm, gate, x, y, y_dtype == CQ_F16, (hipStream_t)stream, epi, up);
   }
+  // Batched decode (2 <= m <= 16, fp16 x, rows of at most 16 columns): one
+  // launch of the column kernel whose tiles hold 8 gate rows and the same 8
+  // up rows, the product formed where the rows' sums are added.
+  if (m >= 2 && m <= 16 && x_dtype == CQ_F16 && gate->format == up->format && knobs().gateup_fused &&
+      knobs().gemvq && gemvq_fits(gate, x) && gemvq_fits(up, x) && gate->k / 256 <= 16) {
+    DeviceModule* dm;
+    cq_status st = device_module(&dm);
+    if (st != CQ_OK) return st;
+    CqEpi epi{};
+    epi.act = act;
+    const cq_weight* ws[2] = {gate, up};
+    void* ys[2] = {y, y};
+    bool declined;
+    st = launch_gemvq(dm, gate, x, m, y, y_dtype == CQ_F16, (hipStream_t)stream, epi, &declined, 2, ws, ys, true);
+    if (!declined) return st;
+  }
   cq_status st = matmul_impl(up, x, x_dtype, m, y, y_dtype, CQ_PATH_AUTO, stream, none);
   if (st != CQ_OK) return st;
   CqEpi epi{};
@@ -1561,6 +1596,21 @@ cq_status cq_matmul_multi(int count, const cq_weight* const* ws, const void* x, 
     cq_status st = device_module(&dm);
     if (st != CQ_OK) return st;
     return launch_gemv1(dm, ws[0], x, ys[0], y_dtype == CQ_F16, (hipStream_t)stream, CqEpi{}, nullptr, count, ws, ys);
+  }
+  // Batched decode (2 <= m <= 16, fp16 x, one format, rows of at most 16
+  // columns, up to 4 weights): one launch of the column kernel over every
+  // weight's tiles, against one activation transit.
+  bool col = m >= 2 && m <= 16 && x_dtype == CQ_F16 && knobs().multi_fused && knobs().gemvq &&
+             count <= kGvqMaxSeg && ws[0]->k / 256 <= 16 && (y_dtype == CQ_F16 || y_dtype == CQ_F32);
+  for (int i = 0; col && i < count; i++) col = ws[i]->format == f && gemvq_fits(ws[i], x);
+  if (col) {
+    DeviceModule* dm;
+    cq_status st = device_module(&dm);
+    if (st != CQ_OK) return st;
+    bool declined;
+    st = launch_gemvq(dm, ws[0], x, m, ys[0], y_dtype == CQ_F16, (hipStream_t)stream, CqEpi{}, &declined, count, ws,
+                      ys);
+    if (!declined) return st;
   }
   for (int i = 0; i < count; i++) {
     const cq_status st = matmul_impl(ws[i], x, x_dtype, m, ys[i], y_dtype, CQ_PATH_AUTO, stream, CqEpi{});

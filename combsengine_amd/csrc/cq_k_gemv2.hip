@@ -27,21 +27,21 @@ GEMV2_FMT(q6_k, CQ_Q6_K)
 
 // Batched decode, K <= 4096: activations loaded once per workgroup, weight
 // columns streamed per wave (cq_gemvq.h).
-#define GEMVQ_KERNEL(NAME, FMT, YT) \
-  extern "C" __global__ void __launch_bounds__(64 * GVQ_MAX_WAVES) NAME(const GvqArgs a) { gemvq_body<FMT, YT>(a); }
-GEMVQ_KERNEL(cq_gemvq_q4_k_yf32, CQ_Q4_K, 0)
-GEMVQ_KERNEL(cq_gemvq_q4_k_yf16, CQ_Q4_K, 1)
-GEMVQ_KERNEL(cq_gemvq_q5_k_yf32, CQ_Q5_K, 0)
-GEMVQ_KERNEL(cq_gemvq_q5_k_yf16, CQ_Q5_K, 1)
-GEMVQ_KERNEL(cq_gemvq_q6_k_yf32, CQ_Q6_K, 0)
-GEMVQ_KERNEL(cq_gemvq_q6_k_yf16, CQ_Q6_K, 1)
-GEMVQ_KERNEL(cq_gemvq_q4_0_yf32, CQ_Q4_0, 0)
-GEMVQ_KERNEL(cq_gemvq_q4_0_yf16, CQ_Q4_0, 1)
-GEMVQ_KERNEL(cq_gemvq_q5_0_yf32, CQ_Q5_0, 0)
-GEMVQ_KERNEL(cq_gemvq_q5_0_yf16, CQ_Q5_0, 1)
-GEMVQ_KERNEL(cq_gemvq_q8_0_yf32, CQ_Q8_0, 0)
-GEMVQ_KERNEL(cq_gemvq_q8_0_yf16, CQ_Q8_0, 1)
-GEMVQ_KERNEL(cq_gemvq_q4_1_yf32, CQ_Q4_1, 0)
-GEMVQ_KERNEL(cq_gemvq_q4_1_yf16, CQ_Q4_1, 1)
-GEMVQ_KERNEL(cq_gemvq_q5_1_yf32, CQ_Q5_1, 0)
-GEMVQ_KERNEL(cq_gemvq_q5_1_yf16, CQ_Q5_1, 1)
+#define GEMVQ_KERNEL(NAME, FMT, YT, MODE) \
+  extern "C" __global__ void __launch_bounds__(64 * GVQ_MAX_WAVES) NAME(const GvqArgs a) { gemvq_body<FMT, YT, MODE>(a); }
+// one weight, several weights (segments), the gated gate / up pair
+#define GEMVQ_FMT(fname, FMT)                                \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_yf32, FMT, 0, 0)           \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_yf16, FMT, 1, 0)           \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_multi_yf32, FMT, 0, 1)     \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_multi_yf16, FMT, 1, 1)     \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_gated_yf32, FMT, 0, 2)     \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_gated_yf16, FMT, 1, 2)
+GEMVQ_FMT(q4_k, CQ_Q4_K)
+GEMVQ_FMT(q5_k, CQ_Q5_K)
+GEMVQ_FMT(q6_k, CQ_Q6_K)
+GEMVQ_FMT(q4_0, CQ_Q4_0)
+GEMVQ_FMT(q5_0, CQ_Q5_0)
+GEMVQ_FMT(q8_0, CQ_Q8_0)
+GEMVQ_FMT(q4_1, CQ_Q4_1)
+GEMVQ_FMT(q5_1, CQ_Q5_1)

@@ -18,6 +18,7 @@ pytestmark = pytest.mark.gpu
 
 FMTS = [QuantFormat.Q4_0, QuantFormat.Q5_0, QuantFormat.Q8_0, QuantFormat.Q4K, QuantFormat.Q5K, QuantFormat.Q6K]
 KQ = [QuantFormat.Q4K, QuantFormat.Q5K, QuantFormat.Q6K]
+ALL_FMTS = FMTS + [QuantFormat.Q4_1, QuantFormat.Q5_1]
 
 
 def _weight(fmt, n, k, seed):
@@ -118,6 +119,32 @@ def test_gate_up_epilogue(cuda, gf, uf, act, m, y_dt):
     O.assert_close(y.float().cpu().numpy(), expect, 1e-3 if y_dt == "f32" else 2e-3)
 
 
+@pytest.mark.parametrize("fmt", ALL_FMTS)
+@pytest.mark.parametrize("n,k", [(300, 4096), (257, 256), (45, 1024), (97, 3584), (50, 768)])
+@pytest.mark.parametrize("m", [2, 7, 16])
+@pytest.mark.parametrize("act", [Activation.Silu, Activation.Gelu])
+def test_gate_up_batched_one_launch(cuda, monkeypatch, fmt, n, k, m, act):
+    """Batched decode of the gated gate / up pair (fp16 h, 2 <= m <= 16): one
+    launch of the column kernel whose tiles hold 8 gate rows and the same 8
+    up rows (ragged last tile: n not a multiple of 8), the product
+    act(fp16(g)) * fp16(u) formed where the rows' sums are added; against the
+    oracle and the two-launch path (COMBS_GATEUP_FUSED=0)."""
+    import torch
+    gd, gw = _weight(fmt, n, k, 70 + int(fmt))
+    ud, uw = _weight(fmt, n, k, 80 + int(fmt))
+    x = _x(m, k, 90 + m)
+    g = O.fused_matmul(int(fmt), gd, x, n, k).astype(np.float16).astype(np.float64)
+    u = O.fused_matmul(int(fmt), ud, x, n, k).astype(np.float16).astype(np.float64)
+    expect = O.activation(int(act), g) * u
+    print(f"gate_up batched {fmt.name} [{n}x{k}] m={m} {act.name}", flush=True)
+    h = torch.from_numpy(x).cuda().half().reshape(1, m, k)
+    y = gated_up(act, QuantLinearOp(gw), QuantLinearOp(uw), h)
+    O.assert_close(y.float().cpu().numpy().reshape(m, n), expect, 2e-3)
+    monkeypatch.setenv("COMBS_GATEUP_FUSED", "0")
+    y2 = gated_up(act, QuantLinearOp(gw), QuantLinearOp(uw), h)
+    O.assert_close(y.float().cpu().numpy(), y2.float().cpu().numpy(), 2e-3, "vs two launches")
+
+
 @pytest.mark.parametrize("split", ["1", "4"])
 def test_gate_up_prefill_split(cuda, monkeypatch, split):
     import torch
@@ -191,7 +218,6 @@ def test_epilogue_single_row_kernels(cuda, monkeypatch, fmt, g2, n, k):
     O.assert_close(g.float().cpu().numpy().reshape(1, n), expect, 2e-3, "gate_up")
 
 
-ALL_FMTS = FMTS + [QuantFormat.Q4_1, QuantFormat.Q5_1]
 
 
 @pytest.mark.parametrize("fmt", ALL_FMTS)
@@ -235,13 +261,15 @@ def test_gate_up_single_row_one_launch(cuda, monkeypatch, fmt, n, k, fused, y_dt
                                  QuantFormat.Q8_0, QuantFormat.Q5_0])
 @pytest.mark.parametrize("ns,k", [((4096, 1024, 1024), 4096), ((512, 128, 128, 64), 1024), ((300, 36), 2304),
                                   ((96,), 16384), ((3584, 512, 512), 3584)])
-@pytest.mark.parametrize("m", [1, 3])
+@pytest.mark.parametrize("m", [1, 3, 9, 16])
 def test_matmul_multi(cuda, monkeypatch, fmt, ns, k, m):
     """Several projections of one input (q / k / v, llama.rs:261-263): one
     launch for decode where every weight's rows fill whole tasks (fp16-register
-    formats), else one call per weight (m = 3, Q5_0, row counts that do not
-    divide the task); each output against the oracle, and equal to the
-    separate launches (COMBS_MULTI_FUSED=0) to the same bar."""
+    formats) at m = 1, one launch of the batched column kernel over every
+    weight's tiles at 2 <= m <= 16 (rows of at most 16 columns: ragged tiles
+    at segment ends, up to 4 weights), else one call per weight; each output
+    against the oracle, and equal to the separate launches
+    (COMBS_MULTI_FUSED=0) to the same bar."""
     import torch
     from combsengine_amd import multi_forward
     ws = [_weight(fmt, n, k, 60 + i + int(fmt)) for i, n in enumerate(ns)]

@@ -137,16 +137,19 @@ typedef enum { CQ_ACT_SILU = 0, CQ_ACT_GELU_TANH = 1, CQ_ACT_GELU = 2 } cq_act;
 /* Gated MLP input projection: y[m,n] = act(x . gate^T) * (x . up^T).
  * Replaces `act::apply(activation, gate.forward(h)) * up.forward(h)`
  * (llama.rs:301-303).  gate and up have the same [n, k] (formats may
- * differ).  up's product is written to y first, in y_dtype, and gate's
- * kernel epilogue reads it back and overwrites it: no scratch memory, two
- * launches on `stream`, one read of x per projection. */
+ * differ).  Decode with fp16 x and one format for both weights is one
+ * launch: m = 1 (K/256 <= 32) and 2 <= m <= 16 (K/256 <= 16, both weights
+ * 16-byte aligned).  Otherwise up's product is written to y first, in
+ * y_dtype, and gate's kernel epilogue reads it back and overwrites it.
+ * No scratch memory on either path. */
 cq_status cq_matmul_gate_up(const cq_weight* gate, const cq_weight* up, const void* x, int x_dtype, int64_t m,
                             int act, void* y, int y_dtype, void* stream);
 
 /* Several projections of one input: ys[i][m, n_i] = x[m,k] . dequant(ws[i])^T
  * for i < count (1..4), every weight with the same k.  Replaces consecutive
  * QuantLinearOp::forward calls on one activation, as the attention block's
- * q / k / v projections (llama.rs:261-263).  Decode (m = 1, fp16 x) of
+ * q / k / v projections (llama.rs:261-263).  Decode (m = 1, and
+ * 2 <= m <= 16 with K/256 <= 16 and 16-byte aligned weights; fp16 x) of
  * weights of one format streams all of them in a single launch; otherwise
  * one cq_matmul per weight, in order, on `stream`. */
 cq_status cq_matmul_multi(int count, const cq_weight* const* ws, const void* x, int x_dtype, int64_t m,

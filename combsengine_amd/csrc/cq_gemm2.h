@@ -47,6 +47,7 @@ typedef __attribute__((address_space(1))) void lt_glb_t;
 
 #define LT_KC 128     // K values per step (half a superblock)
 #define LT_MAXMT 16   // activation tiles per workgroup, at most
+#define LT_RSRC_FLAGS 0x00020000  // buffer resource word 3: raw (stride 0) dword access
 
 struct LtArgs {
   const uint8_t* w;    // packed superblocks, [N rows][row_bytes]
@@ -90,27 +91,59 @@ template <> struct LtFrag<CQ_Q4_K> { typedef LtQ4K T; };
 template <> struct LtFrag<CQ_Q5_K> { typedef LtQ5K T; };
 template <> struct LtFrag<CQ_Q6_K> { typedef LtQ6K T; };
 
+// Fragment loads through a buffer resource: the workgroup's weight rows
+// from a uniform base, the lane's row and lane-group offset in a
+// loop-invariant voffset, the step's superblock in soffset and the field's
+// position as the immediate offset, so no vector arithmetic is spent on
+// addresses inside the K loop.
+typedef __amdgpu_buffer_rsrc_t lt_rsrc_t;
+__device__ __forceinline__ u4v lt_b128(lt_rsrc_t r, uint32_t v, uint32_t so) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, v, so, 0);
+}
+// Per-lane voffsets of one weight row: vr the row, vq the lane group's
+// quant bytes, vh its high-bit (Q5_K) or qh (Q6_K) bytes.
+struct LtVo { uint32_t vr, vq, vh; };
+template <int FMT>
+__device__ __forceinline__ LtVo lt_vo(uint32_t row_off, int g) {
+  if (FMT == CQ_Q6_K) return {row_off, row_off + 32 * (g & 1) + 16 * (g >> 1), row_off + 16 * (g >> 1)};
+  return {row_off, row_off + 32 * (g >> 1) + 16 * (g & 1), row_off + 16 * (g & 1)};
+}
 // Q4_K (gguf.rs:894-925): qs pair p = 2h + (g>>1) holds sub-blocks 2p (low
 // nibbles) and 2p+1 (high); lane group g takes its bytes [16(g&1), +16).
-__device__ __forceinline__ void lt_load(LtQ4K& f, const uint8_t* sb, int h, int g) {
-  f.hdr = ld_u128(sb);
-  f.q = ld_u128(sb + 16 + 64 * h + 32 * (g >> 1) + 16 * (g & 1));
+// The second half (H = 1) uses only the header's scale words: its d / dmin
+// word is not loaded (a load into a register that is then dead lets the
+// compiler reuse that register, which must first wait for the load).
+template <int H>
+__device__ __forceinline__ void lt_hdr(u4v& hdr, lt_rsrc_t r, const LtVo& v, uint32_t so) {
+  if (H == 0) {
+    hdr = lt_b128(r, v.vr, so);
+  } else {
+    const auto w = __builtin_amdgcn_raw_buffer_load_b96(r, v.vr + 4, so, 0);
+    hdr = u4v{0u, w[0], w[1], w[2]};
+  }
+}
+template <int H>
+__device__ __forceinline__ void lt_load(LtQ4K& f, lt_rsrc_t r, const LtVo& v, uint32_t so) {
+  lt_hdr<H>(f.hdr, r, v, so);
+  f.q = lt_b128(r, v.vq + 16 + 64 * H, so);
 }
 // Q5_K (gguf.rs:929-961): as Q4_K, plus qh bytes [16(g&1), +16), whose bit
 // b is the 5th bit of sub-block b.
-__device__ __forceinline__ void lt_load(LtQ5K& f, const uint8_t* sb, int h, int g) {
-  f.hdr = ld_u128(sb);
-  f.qh = ld_u128(sb + 16 + 16 * (g & 1));
-  f.q = ld_u128(sb + 48 + 64 * h + 32 * (g >> 1) + 16 * (g & 1));
+template <int H>
+__device__ __forceinline__ void lt_load(LtQ5K& f, lt_rsrc_t r, const LtVo& v, uint32_t so) {
+  lt_hdr<H>(f.hdr, r, v, so);
+  f.qh = lt_b128(r, v.vh + 16, so);
+  f.q = lt_b128(r, v.vq + 48 + 64 * H, so);
 }
 // Q6_K (gguf.rs:968-999): half h; step s covers quadrant t = 2(s>>1) + (g&1)
 // and l = 16(g>>1) + 8(s&1) + 0..7, so ql bytes [64h + 32(g&1) + 16(g>>1), +16)
 // serve both nibble halves and qh bytes [32h + 16(g>>1), +16) all steps.
-__device__ __forceinline__ void lt_load(LtQ6K& f, const uint8_t* sb, int h, int g) {
-  f.ql = ld_u128(sb + 64 * h + 32 * (g & 1) + 16 * (g >> 1));
-  f.qh = ld_u128(sb + 128 + 32 * h + 16 * (g >> 1));
-  f.sc = ld_u64(sb + 192 + 8 * h);
-  f.d = ld_u16(sb + 208);
+template <int H>
+__device__ __forceinline__ void lt_load(LtQ6K& f, lt_rsrc_t r, const LtVo& v, uint32_t so) {
+  f.ql = lt_b128(r, v.vq + 64 * H, so);
+  f.qh = lt_b128(r, v.vh + 128 + 32 * H, so);
+  f.sc = __builtin_amdgcn_raw_buffer_load_b64(r, v.vr + 192 + 8 * H, so, 0);
+  f.d = H == 0 ? __builtin_amdgcn_raw_buffer_load_b16(r, v.vr + 208, so, 0) : 0u;  // d: first half only
 }
 
 __device__ __forceinline__ uint32_t u4_at(const u4v& v, int i) {
@@ -136,7 +169,7 @@ struct LtGemm {
   static constexpr bool Q6 = FMT == CQ_Q6_K;
 
   f4 acc[NT][MT];
-  Frag cur[NT], nxt[NT];
+  Frag fr[2][NT];            // packed bytes of the step of half H in fr[H]
   float deff[NT];            // units of acc
   float kk[NT];              // -64 * dmin / deff of the current superblock
   bool live[NT];             // d != 0 for the current superblock
@@ -144,13 +177,17 @@ struct LtGemm {
   h2 sb[NT], cb[NT];         // steps s >= 2
   h2 sla[NT], cla[NT], slb[NT], clb[NT];  // Q6_K low-scale operands
   h8 bmin[NT];               // K-quant mins of the superblock (lane groups 0, 1)
-  const uint8_t* wr[NT];
+  lt_rsrc_t wrs;             // the workgroup's weight rows from its first superblock
+  LtVo vo[NT];
   int acol[4];               // byte offset of step s's A chunk in a staged row
   int lane, wave, j, g;
 
-  __device__ __forceinline__ void load_w(Frag* f, int i) {
+  // the packed bytes of step i (half H = i & 1) into fr[H]
+  template <int H>
+  __device__ __forceinline__ void load_w(int i) {
+    const uint32_t so = (uint32_t)(i >> 1) * FmtTraits<FMT>::bytes;
 #pragma unroll
-    for (int t = 0; t < NT; t++) lt_load(f[t], wr[t] + (size_t)(i >> 1) * FmtTraits<FMT>::bytes, i & 1, g);
+    for (int t = 0; t < NT; t++) lt_load<H>(fr[H][t], wrs, vo[t], so);
   }
 
   // Operand constants of the step (half H) for tile t; at a superblock's
@@ -159,7 +196,7 @@ struct LtGemm {
   __device__ __forceinline__ float prep(int t) {
     float r = 1.0f;
     if constexpr (!Q6) {
-      const u4v& hd = cur[t].hdr;
+      const u4v& hd = fr[H][t].hdr;
       if (H == 0) {
         const float d = f16_bits_to_f32(hd.x), dmin = f16_bits_to_f32(hd.x >> 16);
         live[t] = d != 0.0f;
@@ -192,7 +229,7 @@ struct LtGemm {
       }
     } else {
       if (H == 0) {
-        const float d = f16_bits_to_f32(cur[t].d);
+        const float d = f16_bits_to_f32(fr[H][t].d);
         live[t] = d != 0.0f;
         const float dn = live[t] ? 16.0f * d : deff[t];
         r = deff[t] * __builtin_amdgcn_rcpf(dn);
@@ -200,8 +237,8 @@ struct LtGemm {
       }
       // scale index (g>>1) + 2t within the half: t = g&1 (s < 2), t + 2 (s >= 2)
       const uint32_t sh = 8 * ((g >> 1) + 2 * (g & 1));
-      const int sc_a = live[t] ? (int)(int8_t)(cur[t].sc.x >> sh) : 0;
-      const int sc_b = live[t] ? (int)(int8_t)(cur[t].sc.y >> sh) : 0;
+      const int sc_a = live[t] ? (int)(int8_t)(fr[H][t].sc.x >> sh) : 0;
+      const int sc_b = live[t] ? (int)(int8_t)(fr[H][t].sc.y >> sh) : 0;
       const int ha = sc_a >> 4, la = sc_a & 15, hb = sc_b >> 4, lb = sc_b & 15;
       // s < 2: value 1024 + v6;  s >= 2: 1024 + 16*v6
       sa[t] = hsplat((float)ha);
@@ -220,7 +257,7 @@ struct LtGemm {
   // bytes (low / high nibbles), decoded together at s < 2.
   template <int H>
   __device__ __forceinline__ void decode(int t, int s, h8& b, h8& b2, h8& bl) const {
-    const Frag& f = cur[t];
+    const Frag& f = fr[H][t];
     const int wi = 2 * (s & 1);
     if constexpr (FMT == CQ_Q4_K) {
       const uint32_t w0 = u4_at(f.q, wi), w1 = u4_at(f.q, wi + 1);
@@ -385,10 +422,14 @@ __device__ __forceinline__ void gemm2_body(const LtArgs& a) {
   // K slice of this workgroup: superblocks [ub, ub + nu)
   const int ub = blockIdx.z * a.usplit;
   const int nu = min(a.usplit, a.units - ub);
+  const int wg_row0 = bx * NW * 16 * NT;  // < N: the grid covers the rows
+  s.wrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(a.w + (size_t)wg_row0 * a.row_bytes + (size_t)ub * FmtTraits<FMT>::bytes), (short)0, 0x7fffffff,
+      LT_RSRC_FLAGS);
 #pragma unroll
   for (int t = 0; t < NT; t++) {
     const int row = min(n0 + 16 * t + s.j, a.N - 1);
-    s.wr[t] = a.w + (size_t)row * a.row_bytes + (size_t)ub * FmtTraits<FMT>::bytes;
+    s.vo[t] = lt_vo<FMT>((uint32_t)((row - wg_row0) * a.row_bytes), s.g);
     s.deff[t] = 1.0f;
     s.kk[t] = 0.0f;
     s.live[t] = true;
@@ -403,7 +444,9 @@ __device__ __forceinline__ void gemm2_body(const LtArgs& a) {
   // 16 B each); this wave issues i = wave + NW ii.  Lane (row r, slot v)
   // fetches the row's chunk v ^ lt_sw(r); r & 15 does not depend on ii.
   // 32-bit offsets (M * K * 2 < 2^31 is checked by the host) from a uniform
-  // base: the saddr + voffset form of the load.
+  // base.  global_load_lds, not the buffer form: with it the compiler sees
+  // which LDS array a DMA writes and lets the reads of the other array run
+  // while it is in flight (for buffer-to-LDS loads it waits for them).
   const uint32_t K2 = (uint32_t)a.K * 2;
   const uint32_t dr = 4 * s.wave + (s.lane >> 4);
   const uint32_t dsw = 16 * ((s.lane & 15) ^ lt_sw<FMT>(dr));
@@ -432,7 +475,7 @@ __device__ __forceinline__ void gemm2_body(const LtArgs& a) {
   const bool kq = FMT != CQ_Q6_K;
   dma_x(lt_x0, 0);
   if (kq) dma_s(lt_s0, 0);
-  s.load_w(s.cur, 0);
+  s.template load_w<0>(0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
@@ -447,12 +490,10 @@ __device__ __forceinline__ void gemm2_body(const LtArgs& a) {
     if (more) {
       dma_x(xn, i + 1);
       if (kq && H == 1) dma_s(P ? lt_s0 : lt_s1, (i + 1) >> 1);
-      s.load_w(s.nxt, i + 1);
+      s.template load_w<1 - H>(i + 1);
     }
     s.template compute<H>(xc, P ? lt_s1 : lt_s0);
     if (more) {
-#pragma unroll
-      for (int t = 0; t < NT; t++) s.cur[t] = s.nxt[t];
       // this wave's DMA for step i+1 has landed (the weight loads issued
       // behind it were issued a whole step ago and are normally complete)
       __builtin_amdgcn_s_waitcnt(0);

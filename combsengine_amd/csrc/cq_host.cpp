@@ -251,7 +251,8 @@ struct DeviceModule {
   hipFunction_t gemvr[2][4] = {};  // Q4_K rows split across lanes: [y f16][log2 activation pieces per thread]
   int cus = 0;                        // compute units of the device
   // Scratch kept across calls: [0] batched decode slice partials, [1] the
-  // fp32-activation split (whose inner call may take [0]).  Grown on
+  // fp32-activation split (whose inner call may take [0] or [2]), [2] the
+  // prefill GEMMs' activation sums and split partials.  Grown on
   // demand, never freed before the process ends; `ev` is recorded on the
   // stream of each use, and a call on another stream waits for it first.
   struct {
@@ -261,7 +262,7 @@ struct DeviceModule {
     hipEvent_t ev = nullptr;
     hipStream_t last = nullptr;
     bool used = false;
-  } kept[2];
+  } kept[3];
 };
 DeviceModule g_dev[kMaxDevices];
 
@@ -1231,9 +1232,9 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
     while (gx * mblk * splits * 2 <= slots && a.units / (splits * 2) >= 3) splits *= 2;
   }
   if (splits > a.units) splits = a.units;
-  // Scratch: activation sums (Q4_K/Q5_K), then split partials; stream-ordered
-  // (hipMallocAsync), or the fixed buffer of cq_matmul_noalloc, where the
-  // split count halves until the partials fit.
+  // Scratch: activation sums (Q4_K/Q5_K), then split partials; the device's
+  // kept scratch (slot 2), or the fixed buffer of cq_matmul_noalloc, where
+  // the split count halves until the partials fit.
   const size_t sums_bytes = w->format != CQ_Q6_K ? (size_t)m * a.units * 32 : 0;
   auto part_size = [&](int sp) -> size_t {
     const int us = (a.units + sp - 1) / sp;
@@ -1253,10 +1254,7 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
   a.usplit = (a.units + splits - 1) / splits;
   splits = (a.units + a.usplit - 1) / a.usplit;
   const size_t part_bytes = splits > 1 ? (size_t)splits * m * w->n * 4 : 0;
-  void* ws = nullptr;
-  if (fixed) ws = fixed->ptr;
-  else if ((sums_bytes + part_bytes) && !g_plan) HIP_TRY(hipMallocAsync(&ws, sums_bytes + part_bytes, s));
-  auto launch_all = [&]() -> hipError_t {
+  auto launch_all = [&](void* ws) -> hipError_t {
     hipError_t e;
     if (sums_bytes) {
       a.xs = ws;
@@ -1277,8 +1275,18 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
     void* rp[] = {&a.part, &y, &splits, &mn, &n, &ep};
     return klaunch(dm, dm->reduce[yt], (unsigned)((mn + 255) / 256), 1, 1, 256, 0, s, rp);
   };
-  const hipError_t e = launch_all();
-  if (ws && !fixed) HIP_TRY(hipFreeAsync(ws, s));
+  hipError_t e;
+  if (fixed) e = launch_all(fixed->ptr);
+  else if (g_plan || !(sums_bytes + part_bytes)) e = launch_all(reinterpret_cast<void*>(static_cast<uintptr_t>(256)));
+  else if (cs != hipStreamCaptureStatusNone) {
+    // captured, sums beyond the fixed buffer: a graph allocation
+    void* ws;
+    HIP_TRY(hipMallocAsync(&ws, sums_bytes + part_bytes, s));
+    e = launch_all(ws);
+    HIP_TRY(hipFreeAsync(ws, s));
+  } else {
+    e = with_kept_scratch(dm, 2, s, sums_bytes + part_bytes, launch_all);
+  }
   if (e != hipSuccess) return fail(CQ_ERR_HIP, "prefill GEMM launch: %s", hipGetErrorString(e));
   return CQ_OK;
 }
@@ -1311,8 +1319,8 @@ static cq_status launch_gemml(DeviceModule* dm, const cq_weight* w, const void* 
   if (gx > 0x7fffffffLL || mblk > 65535) return fail(CQ_ERR_BAD_SHAPE, "grid too large");
   // K slices while the grid leaves compute units idle (two workgroups fit
   // on one), each of at least 3 steps; COMBS_GEMML_SPLIT forces the count.
-  // Partials from the stream-ordered pool, or the fixed buffer while
-  // capturing and in cq_matmul_noalloc (the split halves until they fit).
+  // Partials from the device's kept scratch (slot 2), or the fixed buffer
+  // while capturing and in cq_matmul_noalloc (the split halves until they fit).
   const int steps = (a.blocks + 3) / 4;  // steps of four blocks (the kernel's LB)
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   if (!g_plan) HIP_TRY(hipStreamIsCapturing(s, &cs));
@@ -1334,23 +1342,25 @@ static cq_status launch_gemml(DeviceModule* dm, const cq_weight* w, const void* 
   a.ssteps = (steps + splits - 1) / splits;
   splits = (steps + a.ssteps - 1) / a.ssteps;
   const size_t part_bytes = part_size(splits);
-  void* ws = nullptr;
-  if (part_bytes) {
-    if (fixed) ws = fixed->ptr;
-    else if (!g_plan) HIP_TRY(hipMallocAsync(&ws, part_bytes, s));
-    a.part = (float*)ws;
-  }
-  void* params[] = {&a};
-  hipError_t e = klaunch(dm, dm->gemml[fi][nt - 1][yt], (unsigned)gx, (unsigned)mblk, (unsigned)splits, 256, 0, s,
-                         params);
-  if (e == hipSuccess && part_bytes) {
-    long long mn = m * w->n;
-    int n = (int)w->n;
-    CqEpi ep = epi;
-    void* rp[] = {&a.part, &y, &splits, &mn, &n, &ep};
-    e = klaunch(dm, dm->reduce[yt], (unsigned)((mn + 255) / 256), 1, 1, 256, 0, s, rp);
-  }
-  if (ws && !fixed) HIP_TRY(hipFreeAsync(ws, s));
+  auto launch_all = [&](void* ws) -> hipError_t {
+    if (part_bytes) a.part = (float*)ws;
+    void* params[] = {&a};
+    hipError_t e = klaunch(dm, dm->gemml[fi][nt - 1][yt], (unsigned)gx, (unsigned)mblk, (unsigned)splits, 256, 0, s,
+                           params);
+    if (e == hipSuccess && part_bytes) {
+      long long mn = m * w->n;
+      int n = (int)w->n;
+      CqEpi ep = epi;
+      void* rp[] = {&a.part, &y, &splits, &mn, &n, &ep};
+      e = klaunch(dm, dm->reduce[yt], (unsigned)((mn + 255) / 256), 1, 1, 256, 0, s, rp);
+    }
+    return e;
+  };
+  // a captured launch without the fixed buffer takes no split (no partials)
+  hipError_t e;
+  if (fixed) e = launch_all(fixed->ptr);
+  else if (g_plan || !part_bytes) e = launch_all(reinterpret_cast<void*>(static_cast<uintptr_t>(256)));
+  else e = with_kept_scratch(dm, 2, s, part_bytes, launch_all);
   if (e != hipSuccess) return fail(CQ_ERR_HIP, "legacy prefill launch: %s", hipGetErrorString(e));
   return CQ_OK;
 }

@@ -167,6 +167,11 @@ template <int FMT, int YT, int NT, int MT>
 struct LtGemm {
   typedef typename LtFrag<FMT>::T Frag;
   static constexpr bool Q6 = FMT == CQ_Q6_K;
+  // MT = 16 runs two waves per SIMD with 128 accumulator registers: it
+  // trades a little VALU for registers (Q4_K high-nibble operands decoded
+  // again at steps 2, 3 instead of kept; the mins built where they are used;
+  // a shorter A-fragment ring).
+  static constexpr bool LEAN = MT >= 16;
 
   f4 acc[NT][MT];
   Frag fr[2][NT];            // packed bytes of the step of half H in fr[H]
@@ -188,6 +193,20 @@ struct LtGemm {
     const uint32_t so = (uint32_t)(i >> 1) * FmtTraits<FMT>::bytes;
 #pragma unroll
     for (int t = 0; t < NT; t++) lt_load<H>(fr[H][t], wrs, vo[t], so);
+  }
+
+  // The superblock's 8 mins as exact fp16 for lane groups 0 and 1 (zero
+  // elsewhere), from the header of the second half's fragment.
+  __device__ __forceinline__ h8 mins(int t) const {
+    const u4v& hd = fr[1][t].hdr;
+    const uint32_t m03 = hd.z & 0x3F3F3F3Fu;
+    const uint32_t m47 = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+    const h2 one = hsplat(1.0f), off = hsplat(-1024.0f);
+    uint32_t u[4] = {pk_fma(perm(C64, m03, SEL_B0_E_B1_E), one, off), pk_fma(perm(C64, m03, SEL_B2_E_B3_E), one, off),
+                     pk_fma(perm(C64, m47, SEL_B0_E_B1_E), one, off), pk_fma(perm(C64, m47, SEL_B2_E_B3_E), one, off)};
+#pragma unroll
+    for (int i = 0; i < 4; i++) u[i] = g < 2 ? u[i] : 0u;
+    return mk_h8(u[0], u[1], u[2], u[3]);
   }
 
   // Operand constants of the step (half H) for tile t; at a superblock's
@@ -216,17 +235,7 @@ struct LtGemm {
       ca[t] = hsplat(-1024.0f * f0);       // (1024 + q) * sc - 1024 sc
       sb[t] = hsplat(f1 * 0.0625f);
       cb[t] = hsplat(-64.0f * f1);         // (1024 + 16 q) * sc/16 - 64 sc
-      if (H == 1) {
-        // the 8 mins as exact fp16 for lane groups 0 and 1 (zero elsewhere)
-        const uint32_t m03 = hd.z & 0x3F3F3F3Fu;
-        const uint32_t m47 = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
-        const h2 one = hsplat(1.0f), off = hsplat(-1024.0f);
-        uint32_t u[4] = {pk_fma(perm(C64, m03, SEL_B0_E_B1_E), one, off), pk_fma(perm(C64, m03, SEL_B2_E_B3_E), one, off),
-                         pk_fma(perm(C64, m47, SEL_B0_E_B1_E), one, off), pk_fma(perm(C64, m47, SEL_B2_E_B3_E), one, off)};
-#pragma unroll
-        for (int i = 0; i < 4; i++) u[i] = g < 2 ? u[i] : 0u;
-        bmin[t] = mk_h8(u[0], u[1], u[2], u[3]);
-      }
+      if (H == 1 && !LEAN) bmin[t] = mins(t);
     } else {
       if (H == 0) {
         const float d = f16_bits_to_f32(fr[H][t].d);
@@ -325,11 +334,12 @@ struct LtGemm {
 #pragma unroll
     for (int t = 0; t < NT; t++) r[t] = prep<H>(t);
     const char* xr = (const char*)(X + j * LT_KC);
-    // A fragments: a ring of MT/2 registers.  Tile tm's fragment of step s
-    // sits in slot tm % (MT/2); once its MFMAs are issued the slot is
-    // reloaded with the fragment needed MT/2 tiles later (tile tm + MT/2 of
-    // this step, or tile tm - MT/2 of the next), MT MFMAs ahead of its use.
-    constexpr int HR = MT / 2;
+    // A fragments: a ring of HR registers (MT/2, at most 4).  Tile tm's
+    // fragment of step s sits in slot tm % HR; once its MFMAs are issued the
+    // slot is reloaded with the fragment needed HR tiles later (tile tm + HR
+    // of this step, or tile tm + HR - MT of the next), NT * HR MFMAs ahead of
+    // its use.
+    constexpr int HR = LEAN ? 2 : MT / 2 < 4 ? MT / 2 : 4;
     auto afrag = [&](int s, int tm) { return *(const h8*)(xr + tm * 16 * LT_KC * 2 + acol[s]); };
     h8 av[HR];
 #pragma unroll
@@ -340,12 +350,15 @@ struct LtGemm {
       h8 b[NT], bl[NT];
 #pragma unroll
       for (int t = 0; t < NT; t++) {
-        if (FMT == CQ_Q4_K && s >= 2) {
+        if (FMT == CQ_Q4_K && s >= 2 && LEAN) {
+          h8 lo;
+          decode<H>(t, s - 2, lo, b[t], bl[t]);  // the same bytes' high nibbles
+        } else if (FMT == CQ_Q4_K && s >= 2) {
           b[t] = bsave[s & 1][t];
         } else {
           h8 b2;
           decode<H>(t, s, b[t], b2, bl[t]);
-          if (FMT == CQ_Q4_K) bsave[s & 1][t] = b2;
+          if (FMT == CQ_Q4_K && !LEAN) bsave[s & 1][t] = b2;
         }
       }
 #pragma unroll
@@ -363,8 +376,10 @@ struct LtGemm {
 #pragma unroll
           for (int t = 0; t < NT; t++) acc[t][tm] = mfma(av[slot], bl[t], acc[t][tm]);
         }
-        if (tm < HR) av[slot] = afrag(s, tm + HR);
-        else if (s < 3) av[slot] = afrag(s + 1, tm - HR);
+        if (tm + HR < MT) av[slot] = afrag(s, tm + HR);
+        else if (s < 3) av[slot] = afrag(s + 1, tm + HR - MT);
+        // LEAN: no fragment read moves above its ring slot's last use
+        if constexpr (LEAN) __builtin_amdgcn_sched_barrier(0);
       }
       // keep each step's decode next to its MFMAs
       __builtin_amdgcn_sched_barrier(0);
@@ -379,7 +394,7 @@ struct LtGemm {
           const h8 as = *(const h8*)(S + (16 * tm + j) * 16 + 8 * (g & 1));
 #pragma unroll
           for (int t = 0; t < NT; t++) {
-            const f4 cm = mfma(as, bmin[t], zero4);
+            const f4 cm = mfma(as, LEAN ? mins(t) : bmin[t], zero4);
 #pragma unroll
             for (int q = 0; q < 4; q++) acc[t][tm][q] = __builtin_fmaf(kk[t], cm[q], acc[t][tm][q]);
           }

@@ -1194,17 +1194,37 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
   a.part = nullptr;
   a.usplit = a.units;
   a.epi = epi;
+  // MT = 8 (128 activation rows, two 4-wave workgroups per compute unit);
+  // Q6_K MT = 16 (256 rows, one 8-wave workgroup per compute unit) with one
+  // weight tile per wave: each decoded operand then serves 16 activation
+  // tiles, which pays for Q6_K's two-MFMA operands (4096 x 14336 at
+  // m = 512 / 2048: 120 / 391 us against 131 / 439), not for Q4_K / Q5_K
+  // (357 against 293 us at m = 2048).  Taken when its workgroups (K split
+  // as below) fill at least 80 % of their last round of compute units:
+  // 512 x 3584 (16-128 workgroups) stays on MT = 8 (21-32 us against 39-43),
+  // as does 18944 x 3584 at m = 512 (296 workgroups: 173 against 200 us).
   int mt = knobs().gemm2_mt;
+  bool q6_wide = false;
+  if (mt == 0 && w->format == CQ_Q6_K && m >= 256) {
+    const long long t16 = (w->n + 127) / 128 * ((m + 255) / 256);
+    long long sp = 1;
+    while (t16 * sp * 2 <= dm->cus && a.units / (sp * 2) >= 3) sp *= 2;
+    const long long wgs = t16 * sp, rounds = (wgs + dm->cus - 1) / dm->cus;
+    q6_wide = wgs * 5 >= rounds * dm->cus * 4;
+  }
+  if (q6_wide) mt = 16;
   if (mt != 8 && mt != 16) mt = 8;
-  const int nw = 4;  // waves per workgroup (the kernels' launch bounds)
-  const long long slots = (long long)dm->cus * (mt == 8 && nw == 4 ? 2 : 1);
+  // waves per workgroup (the kernels' launch bounds): MT = 16 tiles are one
+  // 8-wave workgroup per compute unit, MT = 8 two 4-wave workgroups
+  const int nw = mt == 16 ? 8 : 4;
+  const long long slots = (long long)dm->cus * (mt == 8 ? 2 : 1);
   const long long mblk = (m + 16 * mt - 1) / (16 * mt);
   int nt = knobs().gemm2_nt;
   // NT = 2 while it fills half the slots; Q6_K (long K per superblock pass)
   // already from three eighths (3584 x 18944 at m = 512: 165 against 173 us;
   // Q4_K 14336 x 4096 at m = 128 stays faster with one tile, 46.6 against 50.9).
   const long long fill = (w->n + 16 * nw - 1) / (16 * nw) * mblk * 2;
-  if (nt != 1 && nt != 2) nt = (w->format == CQ_Q6_K ? fill * 4 >= slots * 3 : fill >= slots) ? 2 : 1;
+  if (nt != 1 && nt != 2) nt = q6_wide ? 1 : (w->format == CQ_Q6_K ? fill * 4 >= slots * 3 : fill >= slots) ? 2 : 1;
   const long long gx = (w->n + 16 * nw * nt - 1) / (16 * nw * nt);
   if (gx > 0x7fffffffLL || mblk > 65535) return fail(CQ_ERR_BAD_SHAPE, "grid too large");
   // Split K when the tiles leave compute units idle (each slice keeps >= 3

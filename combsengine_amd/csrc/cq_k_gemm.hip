@@ -26,11 +26,11 @@ GEMM_FMT(q6_k, CQ_Q6_K)
 // unit when each wave fits 256 registers (two waves per SIMD).  (One 8-wave
 // workgroup sharing the activation tile measured the same.)
 #define GEMM2_KERNEL_NW(NAME, FMT, YT, NT, MT, NW)                                                        \
-  extern "C" __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(MT == 8 ? 2 : 1))) \
+  extern "C" __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2))) \
   NAME(const LtArgs a) {                                                                                    \
     gemm2_body<FMT, YT, NT, MT, NW>(a);                                                                     \
   }
-#define GEMM2_KERNEL(NAME, FMT, YT, NT, MT) GEMM2_KERNEL_NW(NAME, FMT, YT, NT, MT, 4)
+#define GEMM2_KERNEL(NAME, FMT, YT, NT, MT) GEMM2_KERNEL_NW(NAME, FMT, YT, NT, MT, (MT == 16 ? 8 : 4))
 GEMM2_KERNEL(cq_gemm2_q4_k_n1_m8_yf32, CQ_Q4_K, 0, 1, 8)
 GEMM2_KERNEL(cq_gemm2_q4_k_n1_m8_yf16, CQ_Q4_K, 1, 1, 8)
 GEMM2_KERNEL(cq_gemm2_q4_k_n1_m16_yf32, CQ_Q4_K, 0, 1, 16)

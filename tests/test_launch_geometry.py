@@ -199,3 +199,66 @@ def test_gemm2_scratch_offsets(N, K, M, fmt):
     assert covered == list(range(units))
     if part:  # reduce: part[z * mn + i]
         assert ((splits - 1) * M * N + M * N) * 4 == part
+
+
+SB_BYTES = {"q4_k": 144, "q5_k": 176, "q6_k": 210}
+
+
+def gemm2_tile_host(fmt, M, N, K, cus=256):
+    """launch_gemm2's tile choice (cq_host.cpp): (mt, nt, nw)."""
+    units = K // 256
+    wide = False
+    if fmt == "q6_k" and M >= 256:
+        t16 = -(-N // 128) * -(-M // 256)
+        sp = 1
+        while t16 * sp * 2 <= cus and units // (sp * 2) >= 3:
+            sp *= 2
+        wgs = t16 * sp
+        rounds = -(-wgs // cus)
+        wide = wgs * 5 >= rounds * cus * 4
+    mt = 16 if wide else 8
+    nw = 8 if mt == 16 else 4
+    slots = cus * (2 if mt == 8 else 1)
+    mblk = -(-M // (16 * mt))
+    fill = -(-N // (16 * nw)) * mblk * 2
+    if wide:
+        nt = 1
+    elif fmt == "q6_k":
+        nt = 2 if fill * 4 >= slots * 3 else 1
+    else:
+        nt = 2 if fill >= slots else 1
+    return mt, nt, nw
+
+
+@pytest.mark.parametrize("N,K,M,wide", [(4096, 14336, 512, True), (4096, 14336, 2048, True),
+                                        (3584, 18944, 512, True), (14336, 4096, 256, True),
+                                        (512, 3584, 512, False), (3584, 3584, 256, False),
+                                        (18944, 3584, 512, False), (4096, 14336, 128, False)])
+def test_gemm2_q6k_tile_choice(N, K, M, wide):
+    # the Q6_K shapes measured for the MT = 16 rule (cq_host.cpp)
+    mt, nt, nw = gemm2_tile_host("q6_k", M, N, K)
+    assert (mt == 16) == wide
+    if wide:
+        assert (nt, nw) == (1, 8)
+
+
+@pytest.mark.parametrize("fmt", ["q4_k", "q5_k", "q6_k"])
+@pytest.mark.parametrize("mt,nt,nw", [(8, 1, 4), (8, 2, 4), (16, 1, 8), (16, 2, 8)])
+@pytest.mark.parametrize("N,K", [(4096, 14336), (128256, 4096), (200, 2560), (3584, 65536)])
+def test_gemm2_dma_cover_and_buffer_offsets(fmt, mt, nt, nw, N, K):
+    # gemm2_body: activation DMA instruction i = wave + NW ii moves staged
+    # rows 4i .. 4i + 3; the sums DMA instruction i < MT/2 moves rows
+    # 32i .. 32i + 31; together they cover the workgroup's 16 MT rows once
+    rows = sorted(4 * (wave + nw * ii) + r for wave in range(nw) for ii in range(4 * mt // nw) for r in range(4))
+    assert rows == list(range(16 * mt))
+    srows = sorted(32 * (wave + nw * ii) + r for wave in range(nw) for ii in range((mt // 2 + nw - 1) // nw)
+                   if wave + nw * ii < mt // 2 for r in range(32))
+    assert srows == list(range(16 * mt))
+    # weight buffer loads: base = the workgroup's first row and slice; the
+    # largest voffset + immediate + soffset stays under the 2^31 records
+    units = K // 256
+    row_bytes = units * SB_BYTES[fmt]
+    rows_wg = nw * 16 * nt
+    lane_max = {"q4_k": 32 + 16 + 16 + 64, "q5_k": 32 + 16 + 48 + 64, "q6_k": 208}[fmt]
+    top = (rows_wg - 1) * row_bytes + lane_max + 16 + (units - 1) * SB_BYTES[fmt]
+    assert top < 2 ** 31

@@ -6,11 +6,14 @@
 // cycles, a wave64 VALU op about 4), so the VALU work per MFMA, more than
 // the MFMA count, sets the speed.  Everything below minimises it:
 //
-//   - Workgroup tile: 16*MT activation rows (MT = 16: 256) x 4 waves x NT
-//     16-row weight tiles.  Each wave decodes only its own NT weight tiles,
-//     straight from packed bytes in registers into exact fp16 MFMA operands
-//     (q*sc, as in the decode GEMV), and reuses every decoded operand for MT
-//     MFMAs, one per activation tile.
+//   - Workgroup tile: 16*MT activation rows x NW waves x NT 16-row weight
+//     tiles (MT = 8: 128 rows, 4 waves, two workgroups per compute unit;
+//     MT = 16: 256 rows, 8 waves, one).  Each wave decodes only its own NT
+//     weight tiles, straight from packed bytes in registers into exact fp16
+//     MFMA operands (q*sc, as in the decode GEMV), and reuses every decoded
+//     operand for MT MFMAs, one per activation tile.  The packed bytes come
+//     by buffer loads whose addresses cost no vector instructions in the K
+//     loop (row offsets fixed per lane, the step in the scalar offset).
 //   - Steps are half superblocks (128 K values), so two activation chunks
 //     (up to 256 rows x 128 halves, 64 KB) double-buffer in LDS.  They arrive
 //     by global_load_lds (LDS DMA) one step ahead, XOR-swizzled per row so

@@ -105,10 +105,10 @@ const void* cq_weight_device_ptr(const cq_weight* w);
  * fp32 activations must be finite and below 65504 in magnitude (they are fed
  * to the fp16 matrix cores as a hi+lo pair; at m >= 2 -- m >= 4 for the
  * K-quants -- that split is made once into 2m fp16 rows that the fp16
- * kernels multiply in one pass).  Prefill (m > 16) takes stream-ordered
- * scratch (activation sums, split partials); batched decode (2 <= m <= 16)
- * of rows longer than 4096 values and the fp32 split take a per-device
- * buffer kept across calls (ordered across streams by an event).  While
+ * kernels multiply in one pass).  Prefill (m > 16; activation sums, split
+ * partials), batched decode (2 <= m <= 16) of rows longer than 4096 values
+ * and the fp32 split each take a per-device buffer kept across calls
+ * (ordered across streams by an event).  While
  * the stream is being captured into a HIP graph, prefill and batched
  * decode take the device's fixed array instead (see cq_matmul_noalloc),
  * which graphs captured this way share: replays that overlap on one device

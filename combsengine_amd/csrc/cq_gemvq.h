@@ -115,15 +115,82 @@ __device__ __forceinline__ void gvq_apos(int g, int s, int& p0, int& o0, int& p1
   }
 }
 
+// Q4_K / Q5_K min term: the wave's column is fixed for the launch, so its
+// sub-block activation sums are formed once (as sum / 64, fp16 hi + lo, so
+// no fp16 overflows), in the A layout of a 16x16x16 MFMA: lane group 0 / 1
+// holds the hi halves of sub-blocks 0-3 / 4-7, group 2 / 3 the lo halves.
+// Lane (row j, group g) of the fragments holds k = 64 g + 8 s: sub-block 2g
+// (s < 4) and 2g + 1 (s >= 4); the rearrangement is two lane shuffles.
+__device__ __forceinline__ h4 gvq_xsums(const h8 (&xa)[8], int lane) {
+  const h2 one = {1, 1};
+  float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+  for (int s = 0; s < 8; s++) {
+    const u4v v = __builtin_bit_cast(u4v, xa[s]);
+    float t = __builtin_amdgcn_fdot2(as_h2(v.x), one, 0.0f, false);
+    t = __builtin_amdgcn_fdot2(as_h2(v.y), one, t, false);
+    t = __builtin_amdgcn_fdot2(as_h2(v.z), one, t, false);
+    t = __builtin_amdgcn_fdot2(as_h2(v.w), one, t, false);
+    if (s < 4) s0 += t;
+    else s1 += t;
+  }
+  const int j = lane & 15, g = lane >> 4, hh = g & 1;
+  // sub-blocks 4 hh + 0, 1 from group 2 hh; 4 hh + 2, 3 from group 2 hh + 1
+  const int la = 16 * (2 * hh) + j, lb = la + 16;
+  const float v[4] = {__shfl(s0, la, 64) * 0.015625f, __shfl(s1, la, 64) * 0.015625f,
+                      __shfl(s0, lb, 64) * 0.015625f, __shfl(s1, lb, 64) * 0.015625f};
+  h4 r;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const _Float16 hi = (_Float16)v[e];
+    r[e] = g < 2 ? hi : (_Float16)(v[e] - (float)hi);
+  }
+  return r;
+}
+// B operand for that MFMA: the 6-bit mins of sub-blocks 4 (g & 1) + 0..3 as
+// exact fp16 (1024 + m under the fp16 exponent, less 1024).
+__device__ __forceinline__ h4 gvq_mins(const u4v& hdr, int g) {
+  const uint32_t m03 = hdr.z & 0x3F3F3F3Fu;
+  const uint32_t m47 = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
+  const uint32_t mm = (g & 1) ? m47 : m03;
+  const h2 one = hsplat(1.0f), off = hsplat(-1024.0f);
+  const uint32_t a = pk_fma(perm(C64, mm, SEL_B0_E_B1_E), one, off);
+  const uint32_t b = pk_fma(perm(C64, mm, SEL_B2_E_B3_E), one, off);
+  return __builtin_bit_cast(h4, u2v{a, b});
+}
+
 // One column of one 16-row tile against the lane's 8 A fragments (legacy:
 // block s meets fragment s; every block's fp16 scale, and the affine
 // formats' min times the block's activation sum, applied to fp32 results).
-template <int FMT>
-__device__ __forceinline__ f4 gvq_column(const uint8_t* wp, const h8 (&xa)[8], int g) {
-  if constexpr (FmtTraits<FMT>::vals == 256) {
+template <int FMT, bool MSUM>
+__device__ __forceinline__ f4 gvq_column(const uint8_t* wp, const h8 (&xa)[8], const h4& xs, int g) {
+  if constexpr (FMT == CQ_Q6_K) {
     typename FmtTraits<FMT>::Frag f;
     load_unit<FMT>(f, wp, g, 0);
     return gvd_superblock<FMT>(f, xa, g);
+  } else if constexpr (FmtTraits<FMT>::vals == 256) {
+    if constexpr (!MSUM) {
+      // min term by 8 MFMAs against the mins (no sums set-up)
+      typename FmtTraits<FMT>::Frag f;
+      load_unit<FMT>(f, wp, g, 0);
+      return gvd_superblock<FMT>(f, xa, g);
+    }
+    // main term by 8 MFMAs on the exact q*sc operands; the min term
+    // sum_sb m_sb * sum(x in sb) by one 16x16x16 MFMA against the column's
+    // sub-block sums / 64
+    typename FmtTraits<FMT>::Frag f;
+    load_unit<FMT>(f, wp, g, 0);
+    DecKQ o;
+    if constexpr (FMT == CQ_Q4_K) decode_q4k(f, g, o);
+    else decode_q5k(f, g, o);
+    f4 c = {0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < 8; s++) c = mfma(xa[s], o.b[s], c);
+    const f4 cm = __builtin_amdgcn_mfma_f32_16x16x16f16(xs, gvq_mins(f.hdr, g), f4{0, 0, 0, 0}, 0, 0, 0);
+    f4 res;
+#pragma unroll
+    for (int r = 0; r < 4; r++) res[r] = __builtin_fmaf(-64.0f * o.dmin, cm[r], o.d * c[r]);
+    return res;
   } else {
     f4 acc = {0, 0, 0, 0};
 #pragma unroll
@@ -148,9 +215,14 @@ __device__ __forceinline__ f4 gvq_column(const uint8_t* wp, const h8 (&xa)[8], i
   }
 }
 
-// MODE 0: one weight (segment 0); 1: segments; 2: gated pair.
-template <int FMT, int YT, int MODE>
+// MODE 0: one weight (segment 0); 1: segments; 2: gated pair.  MSUM (Q4_K /
+// Q5_K): the min term by one MFMA against the column's sub-block sums, whose
+// set-up pays from two tiles per workgroup on (Q4_K 14336 x 4096, 3-4
+// tiles: 12.0-12.5 -> 11.6 us at m = 2; 4096 x 4096, one tile: 6.5 -> 7.0);
+// the host picks it when every workgroup has at least two.
+template <int FMT, int YT, int MODE, bool MSUM>
 __device__ __forceinline__ void gemvq_body(const GvqArgs& a) {
+  static_assert(!MSUM || FMT == CQ_Q4_K || FMT == CQ_Q5_K, "sums for the K-quant min term only");
   typedef GvqShape<FMT> S;
   constexpr int CB = S::CB, PR = S::PR, P = S::P, NI = S::NI, SLOT = S::SLOT, R = S::R, TC = S::TC;
   extern __shared__ __attribute__((aligned(16))) u4v gq_lds[];
@@ -279,6 +351,10 @@ __device__ __forceinline__ void gemvq_body(const GvqArgs& a) {
     asm volatile("" ::: "memory");
   }
 
+  // MSUM: the column's sub-block sums for the K-quant min term (all lanes:
+  // shuffles)
+  h4 xs = {};
+  if constexpr (MSUM) xs = gvq_xsums(xa, lane);
   for (int t = 1; live && t < R - 1 && t < nmine; t++) dma(t);
   // Tiles in chunks of TC: each wave keeps its partial sums of a chunk
   // in registers and the chunk is added across waves afterwards, so that
@@ -300,7 +376,7 @@ __device__ __forceinline__ void gemvq_body(const GvqArgs& a) {
           gv3_wait_vm<0>();
         }
         const uint8_t* wp = (const uint8_t*)ring + SLOT * (t % R) + 16 * PR * j + my_off(t);
-        acc[tt] = gvq_column<FMT>(wp, xa, g);
+        acc[tt] = gvq_column<FMT, MSUM>(wp, xa, xs, g);
         // this slot is refilled in a later iteration: its reads must be done
         __builtin_amdgcn_s_waitcnt(0xC07F);
         asm volatile("" ::: "memory");

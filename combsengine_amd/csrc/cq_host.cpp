@@ -247,6 +247,7 @@ struct DeviceModule {
   hipFunction_t gemvd[kNumFormats][3][2] = {};  // K-quants only: [format][NT 1, 2, 4][y f16]
   hipFunction_t gemvs[kNumFormats][2] = {};  // K-quants only: [format][y f16]
   hipFunction_t gemvq[kNumFormats][3][2] = {};  // [format][one weight, several, gated pair][y f16]
+  hipFunction_t gemvq_ms[kNumFormats][3][2] = {};  // Q4_K / Q5_K: min term against the column's sums
   hipFunction_t gemml[kNumFormats][2][2] = {};  // 32-value formats only: [format][NT - 1][y f16]
   hipFunction_t gemvr[2][4] = {};  // Q4_K rows split across lanes: [y f16][log2 activation pieces per thread]
   int cus = 0;                        // compute units of the device
@@ -404,6 +405,13 @@ void load_module(DeviceModule& d, int dev) {
           d.err = std::string("missing kernel ") + name;
           return;
         }
+        if (kFormats[fi] != CQ_Q4_K && kFormats[fi] != CQ_Q5_K) continue;
+        snprintf(name, sizeof name, "cq_gemvq_%s%s_y%s_ms", fmt_name(kFormats[fi]),
+                 md == 0 ? "" : md == 1 ? "_multi" : "_gated", yt ? "f16" : "f32");
+        if (get(&d.gemvq_ms[fi][md][yt], name) != hipSuccess) {
+          d.err = std::string("missing kernel ") + name;
+          return;
+        }
       }
     }
   for (int fi = 0; fi < kNumFormats; fi++) {
@@ -488,7 +496,7 @@ constexpr int kUnset = -1000000;
 struct Knobs {
   int gemv_waves, gemv1, gemv1k, gemv1_grid, gemv1_i8, gemv1_prefetch2, gemv1_span, gemv1_spread,
       gemv1_wave_major, gemv2, gemv2_wpc, gemvd, gvd_nt, gvd_waves, gemm_kernel, gemm_waves, gemm2_mt,
-      gemm2_nt, gemm2_split, gateup_fused, gemvr, gemvs, gemvs_split, gemvq, gemvq_groups, gemvq_long, f32_split, gemml, gemml_nt, gemml_split,
+      gemm2_nt, gemm2_split, gateup_fused, gemvr, gemvs, gemvs_split, gemvq, gemvq_groups, gemvq_long, gemvq_msum, f32_split, gemml, gemml_nt, gemml_split,
       multi_fused;
 };
 Knobs g_knobs;
@@ -525,6 +533,7 @@ void read_knobs() {
   k.gemvs_split = env_int("COMBS_GEMVS_SPLIT", 0);
   k.gemvq = env_int("COMBS_GEMVQ", 1);
   k.gemvq_groups = env_int("COMBS_GEMVQ_GROUPS", 0);
+  k.gemvq_msum = env_int("COMBS_GEMVQ_MSUM", 1);
   k.gemvq_long = env_int("COMBS_GEMVQ_LONG", 1);
   k.f32_split = env_int("COMBS_F32_SPLIT", 1);
   k.gemml = env_int("COMBS_GEMML", 1);
@@ -907,8 +916,14 @@ static cq_status launch_gemvq(DeviceModule* dm, const cq_weight* w, const void* 
   auto launch_all = [&](void* ws_) -> hipError_t {
     a.part = (float*)ws_;
     void* params[] = {&a};
-    hipError_t e = klaunch(dm, dm->gemvq[fi][gated ? 2 : nseg > 1 ? 1 : 0][yt], (unsigned)groups, (unsigned)slices, 1,
-                           64 * nw, (unsigned)lds, s, params);
+    // Q4_K / Q5_K with at least two tiles per workgroup: the min term
+    // against the column's sub-block sums (_ms), whose set-up then pays
+    const int md = gated ? 2 : nseg > 1 ? 1 : 0;
+    // (COMBS_GEMVQ_MSUM=0 never, 2 always)
+    const bool ms = (w->format == CQ_Q4_K || w->format == CQ_Q5_K) &&
+                    (knobs().gemvq_msum == 2 || (knobs().gemvq_msum == 1 && tiles >= 2 * groups));
+    hipError_t e = klaunch(dm, ms ? dm->gemvq_ms[fi][md][yt] : dm->gemvq[fi][md][yt], (unsigned)groups,
+                           (unsigned)slices, 1, 64 * nw, (unsigned)lds, s, params);
     if (e != hipSuccess || !part_bytes) return e;
     long long mn = m * w->n;
     int n = (int)w->n;

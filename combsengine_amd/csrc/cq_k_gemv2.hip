@@ -27,16 +27,24 @@ GEMV2_FMT(q6_k, CQ_Q6_K)
 
 // Batched decode, K <= 4096: activations loaded once per workgroup, weight
 // columns streamed per wave (cq_gemvq.h).
-#define GEMVQ_KERNEL(NAME, FMT, YT, MODE) \
-  extern "C" __global__ void __launch_bounds__(64 * GVQ_MAX_WAVES) NAME(const GvqArgs a) { gemvq_body<FMT, YT, MODE>(a); }
+#define GEMVQ_KERNEL(NAME, FMT, YT, MODE, MSUM) \
+  extern "C" __global__ void __launch_bounds__(64 * GVQ_MAX_WAVES) NAME(const GvqArgs a) { gemvq_body<FMT, YT, MODE, MSUM>(a); }
 // one weight, several weights (segments), the gated gate / up pair
-#define GEMVQ_FMT(fname, FMT)                                \
-  GEMVQ_KERNEL(cq_gemvq_##fname##_yf32, FMT, 0, 0)           \
-  GEMVQ_KERNEL(cq_gemvq_##fname##_yf16, FMT, 1, 0)           \
-  GEMVQ_KERNEL(cq_gemvq_##fname##_multi_yf32, FMT, 0, 1)     \
-  GEMVQ_KERNEL(cq_gemvq_##fname##_multi_yf16, FMT, 1, 1)     \
-  GEMVQ_KERNEL(cq_gemvq_##fname##_gated_yf32, FMT, 0, 2)     \
-  GEMVQ_KERNEL(cq_gemvq_##fname##_gated_yf16, FMT, 1, 2)
+#define GEMVQ_FMT(fname, FMT)                                       \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_yf32, FMT, 0, 0, false)           \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_yf16, FMT, 1, 0, false)           \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_multi_yf32, FMT, 0, 1, false)     \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_multi_yf16, FMT, 1, 1, false)     \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_gated_yf32, FMT, 0, 2, false)     \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_gated_yf16, FMT, 1, 2, false)
+// Q4_K / Q5_K: the same with the min term against the column's sub-block sums
+#define GEMVQ_FMT_MS(fname, FMT)                                    \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_yf32_ms, FMT, 0, 0, true)         \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_yf16_ms, FMT, 1, 0, true)         \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_multi_yf32_ms, FMT, 0, 1, true)   \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_multi_yf16_ms, FMT, 1, 1, true)   \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_gated_yf32_ms, FMT, 0, 2, true)   \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_gated_yf16_ms, FMT, 1, 2, true)
 GEMVQ_FMT(q4_k, CQ_Q4_K)
 GEMVQ_FMT(q5_k, CQ_Q5_K)
 GEMVQ_FMT(q6_k, CQ_Q6_K)
@@ -45,3 +53,5 @@ GEMVQ_FMT(q5_0, CQ_Q5_0)
 GEMVQ_FMT(q8_0, CQ_Q8_0)
 GEMVQ_FMT(q4_1, CQ_Q4_1)
 GEMVQ_FMT(q5_1, CQ_Q5_1)
+GEMVQ_FMT_MS(q4_k, CQ_Q4_K)
+GEMVQ_FMT_MS(q5_k, CQ_Q5_K)

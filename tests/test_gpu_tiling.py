@@ -142,10 +142,14 @@ def test_gemvd_row_tiles_bit_identical(cuda, monkeypatch, fmt, nw):
 
 @pytest.mark.parametrize("fmt", ALL)
 @pytest.mark.parametrize("m", [3, 16])
-def test_gemvq_groups_bit_identical(cuda, monkeypatch, fmt, m):
+@pytest.mark.parametrize("msum", ["0", "2"])
+def test_gemvq_groups_bit_identical(cuda, monkeypatch, fmt, m, msum):
     """Batched decode through the column kernel: 1, 5, 64 workgroups and the
-    default grid give the same bits."""
+    default grid give the same bits, for each way of forming the Q4_K / Q5_K
+    min term (8 MFMAs against the mins, or one against the column's
+    sub-block sums: COMBS_GEMVQ_MSUM=0 / 2; by default the grid picks)."""
     import torch
+    monkeypatch.setenv("COMBS_GEMVQ_MSUM", msum)
     n, k = 1300, 3584
     data, w = _weight(fmt, n, k, 960 + int(fmt))
     x = torch.from_numpy(_x(m, k, 11)).cuda().half()

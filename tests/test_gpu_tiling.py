@@ -184,3 +184,28 @@ def test_dequant_rounding_blocks_bit_exact(cuda):
         got = dequantize_gpu(fmt, blk.tobytes())
         want = O.dequant(int(fmt), blk.tobytes(), got.size)
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), fmt.name
+
+
+@pytest.mark.parametrize("fmt", [F.Q4K, F.Q5K])
+@pytest.mark.parametrize("m", [2, 9, 16])
+@pytest.mark.parametrize("n,k", [(1300, 3584), (520, 4096), (300, 14336)])
+def test_gemvq_min_term_sums_close(cuda, monkeypatch, fmt, m, n, k):
+    """The batched decode's two ways of forming the Q4_K / Q5_K min term —
+    eight MFMAs of the activations against the mins, or one against the
+    column's sub-block sums (sum / 64 split into fp16 hi + lo) — differ
+    only by the sums' rounding (about 22 bits): the outputs agree to 1e-5 of
+    their scale, far inside the 1e-3 the oracle comparison allows."""
+    import torch
+    data, w = _weight(fmt, n, k, 990 + int(fmt) + m)
+    x = torch.from_numpy(_x(m, k, 12 + m)).cuda().half()
+    outs = {}
+    for ms in ("0", "2"):
+        monkeypatch.setenv("COMBS_GEMVQ_MSUM", ms)
+        y = torch.empty((m, n), device="cuda")
+        w.matmul_into(x, y)
+        torch.cuda.synchronize()
+        outs[ms] = y.cpu().numpy().astype(np.float64)
+    scale = max(np.abs(outs["0"]).max(), 1.0)
+    assert np.abs(outs["0"] - outs["2"]).max() <= 1e-5 * scale
+    wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
+    O.assert_close(outs["2"], _x(m, k, 12 + m).astype(np.float64) @ wd.T.astype(np.float64), 1e-3, "sums")

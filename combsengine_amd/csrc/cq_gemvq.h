@@ -220,8 +220,13 @@ __device__ __forceinline__ f4 gvq_column(const uint8_t* wp, const h8 (&xa)[8], c
 // set-up pays from two tiles per workgroup on (Q4_K 14336 x 4096, 3-4
 // tiles: 12.0-12.5 -> 11.6 us at m = 2; 4096 x 4096, one tile: 6.5 -> 7.0);
 // the host picks it when every workgroup has at least two.
-template <int FMT, int YT, int MODE, bool MSUM>
+// EPI (one weight only): apply the bias / gated epilogue at the store.  Its
+// argument fields otherwise stay live in scalar registers through the tile
+// loop and spill (8-30 SGPRs), so launches without an epilogue take the
+// kernels built without it.
+template <int FMT, int YT, int MODE, bool MSUM, bool EPI>
 __device__ __forceinline__ void gemvq_body(const GvqArgs& a) {
+  static_assert(!EPI || MODE == 0, "the epilogue is for one-weight launches");
   static_assert(!MSUM || FMT == CQ_Q4_K || FMT == CQ_Q5_K, "sums for the K-quant min term only");
   typedef GvqShape<FMT> S;
   constexpr int CB = S::CB, PR = S::PR, P = S::P, NI = S::NI, SLOT = S::SLOT, R = S::R, TC = S::TC;
@@ -420,7 +425,8 @@ __device__ __forceinline__ void gemvq_body(const GvqArgs& a) {
           void* const y = sg.y;
           if (m < a.M && n < N) {
             if (a.part) a.part[((size_t)blockIdx.y * a.M + m) * N + n] = s;
-            else cq_store<YT>(y, a.epi, s, (size_t)m * N + n, n);
+            else if constexpr (EPI) cq_store<YT>(y, a.epi, s, (size_t)m * N + n, n);
+            else cq_store_raw<YT>(y, s, (size_t)m * N + n);
           }
         }
       }

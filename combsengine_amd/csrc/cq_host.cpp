@@ -248,6 +248,7 @@ struct DeviceModule {
   hipFunction_t gemvs[kNumFormats][2] = {};  // K-quants only: [format][y f16]
   hipFunction_t gemvq[kNumFormats][3][2] = {};  // [format][one weight, several, gated pair][y f16]
   hipFunction_t gemvq_ms[kNumFormats][3][2] = {};  // Q4_K / Q5_K: min term against the column's sums
+  hipFunction_t gemvq_epi[kNumFormats][2][2] = {};  // one weight with the epilogue: [format][_ms][y f16]
   hipFunction_t gemml[kNumFormats][2][2] = {};  // 32-value formats only: [format][NT - 1][y f16]
   hipFunction_t gemvr[2][4] = {};  // Q4_K rows split across lanes: [y f16][log2 activation pieces per thread]
   int cus = 0;                        // compute units of the device
@@ -405,12 +406,23 @@ void load_module(DeviceModule& d, int dev) {
           d.err = std::string("missing kernel ") + name;
           return;
         }
-        if (kFormats[fi] != CQ_Q4_K && kFormats[fi] != CQ_Q5_K) continue;
-        snprintf(name, sizeof name, "cq_gemvq_%s%s_y%s_ms", fmt_name(kFormats[fi]),
-                 md == 0 ? "" : md == 1 ? "_multi" : "_gated", yt ? "f16" : "f32");
-        if (get(&d.gemvq_ms[fi][md][yt], name) != hipSuccess) {
-          d.err = std::string("missing kernel ") + name;
-          return;
+        const bool msf = kFormats[fi] == CQ_Q4_K || kFormats[fi] == CQ_Q5_K;
+        for (int ms = 0; ms < (msf ? 2 : 1); ms++) {
+          if (ms) {
+            snprintf(name, sizeof name, "cq_gemvq_%s%s_y%s_ms", fmt_name(kFormats[fi]),
+                     md == 0 ? "" : md == 1 ? "_multi" : "_gated", yt ? "f16" : "f32");
+            if (get(&d.gemvq_ms[fi][md][yt], name) != hipSuccess) {
+              d.err = std::string("missing kernel ") + name;
+              return;
+            }
+          }
+          if (md != 0) continue;
+          snprintf(name, sizeof name, "cq_gemvq_%s_y%s%s_epi", fmt_name(kFormats[fi]), yt ? "f16" : "f32",
+                   ms ? "_ms" : "");
+          if (get(&d.gemvq_epi[fi][ms][yt], name) != hipSuccess) {
+            d.err = std::string("missing kernel ") + name;
+            return;
+          }
         }
       }
     }
@@ -922,8 +934,12 @@ static cq_status launch_gemvq(DeviceModule* dm, const cq_weight* w, const void* 
     // (COMBS_GEMVQ_MSUM=0 never, 2 always)
     const bool ms = (w->format == CQ_Q4_K || w->format == CQ_Q5_K) &&
                     (knobs().gemvq_msum == 2 || (knobs().gemvq_msum == 1 && tiles >= 2 * groups));
-    hipError_t e = klaunch(dm, ms ? dm->gemvq_ms[fi][md][yt] : dm->gemvq[fi][md][yt], (unsigned)groups,
-                           (unsigned)slices, 1, 64 * nw, (unsigned)lds, s, params);
+    // the epilogue (bias, gated product) only where the store applies it: one
+    // weight, not sliced (the slices' reduction applies it instead)
+    const bool use_epi = md == 0 && !part_bytes && (epi.bias || epi.aux);
+    hipFunction_t k =
+        use_epi ? dm->gemvq_epi[fi][ms ? 1 : 0][yt] : ms ? dm->gemvq_ms[fi][md][yt] : dm->gemvq[fi][md][yt];
+    hipError_t e = klaunch(dm, k, (unsigned)groups, (unsigned)slices, 1, 64 * nw, (unsigned)lds, s, params);
     if (e != hipSuccess || !part_bytes) return e;
     long long mn = m * w->n;
     int n = (int)w->n;

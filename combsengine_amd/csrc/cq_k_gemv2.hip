@@ -27,24 +27,29 @@ GEMV2_FMT(q6_k, CQ_Q6_K)
 
 // Batched decode, K <= 4096: activations loaded once per workgroup, weight
 // columns streamed per wave (cq_gemvq.h).
-#define GEMVQ_KERNEL(NAME, FMT, YT, MODE, MSUM) \
-  extern "C" __global__ void __launch_bounds__(64 * GVQ_MAX_WAVES) NAME(const GvqArgs a) { gemvq_body<FMT, YT, MODE, MSUM>(a); }
-// one weight, several weights (segments), the gated gate / up pair
-#define GEMVQ_FMT(fname, FMT)                                       \
-  GEMVQ_KERNEL(cq_gemvq_##fname##_yf32, FMT, 0, 0, false)           \
-  GEMVQ_KERNEL(cq_gemvq_##fname##_yf16, FMT, 1, 0, false)           \
-  GEMVQ_KERNEL(cq_gemvq_##fname##_multi_yf32, FMT, 0, 1, false)     \
-  GEMVQ_KERNEL(cq_gemvq_##fname##_multi_yf16, FMT, 1, 1, false)     \
-  GEMVQ_KERNEL(cq_gemvq_##fname##_gated_yf32, FMT, 0, 2, false)     \
-  GEMVQ_KERNEL(cq_gemvq_##fname##_gated_yf16, FMT, 1, 2, false)
+#define GEMVQ_KERNEL(NAME, FMT, YT, MODE, MSUM, EPI) \
+  extern "C" __global__ void __launch_bounds__(64 * GVQ_MAX_WAVES) NAME(const GvqArgs a) { gemvq_body<FMT, YT, MODE, MSUM, EPI>(a); }
+// one weight (plain, and with the bias / gated epilogue), several weights
+// (segments), the gated gate / up pair
+#define GEMVQ_FMT(fname, FMT)                                              \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_yf32, FMT, 0, 0, false, false)           \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_yf16, FMT, 1, 0, false, false)           \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_yf32_epi, FMT, 0, 0, false, true)        \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_yf16_epi, FMT, 1, 0, false, true)        \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_multi_yf32, FMT, 0, 1, false, false)     \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_multi_yf16, FMT, 1, 1, false, false)     \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_gated_yf32, FMT, 0, 2, false, false)     \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_gated_yf16, FMT, 1, 2, false, false)
 // Q4_K / Q5_K: the same with the min term against the column's sub-block sums
-#define GEMVQ_FMT_MS(fname, FMT)                                    \
-  GEMVQ_KERNEL(cq_gemvq_##fname##_yf32_ms, FMT, 0, 0, true)         \
-  GEMVQ_KERNEL(cq_gemvq_##fname##_yf16_ms, FMT, 1, 0, true)         \
-  GEMVQ_KERNEL(cq_gemvq_##fname##_multi_yf32_ms, FMT, 0, 1, true)   \
-  GEMVQ_KERNEL(cq_gemvq_##fname##_multi_yf16_ms, FMT, 1, 1, true)   \
-  GEMVQ_KERNEL(cq_gemvq_##fname##_gated_yf32_ms, FMT, 0, 2, true)   \
-  GEMVQ_KERNEL(cq_gemvq_##fname##_gated_yf16_ms, FMT, 1, 2, true)
+#define GEMVQ_FMT_MS(fname, FMT)                                           \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_yf32_ms, FMT, 0, 0, true, false)         \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_yf16_ms, FMT, 1, 0, true, false)         \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_yf32_ms_epi, FMT, 0, 0, true, true)      \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_yf16_ms_epi, FMT, 1, 0, true, true)      \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_multi_yf32_ms, FMT, 0, 1, true, false)   \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_multi_yf16_ms, FMT, 1, 1, true, false)   \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_gated_yf32_ms, FMT, 0, 2, true, false)   \
+  GEMVQ_KERNEL(cq_gemvq_##fname##_gated_yf16_ms, FMT, 1, 2, true, false)
 GEMVQ_FMT(q4_k, CQ_Q4_K)
 GEMVQ_FMT(q5_k, CQ_Q5_K)
 GEMVQ_FMT(q6_k, CQ_Q6_K)

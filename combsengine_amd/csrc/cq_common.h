@@ -219,6 +219,22 @@ __device__ __forceinline__ float cq_epi_apply(const CqEpi& e, float v, float b, 
   if (e.aux) v = cq_act(v, e.act) * u;
   return v;
 }
+// The epilogue with the activation fixed at compile time (ACT < 0: bias
+// only): kernels that store many outputs per thread pick the activation
+// once, instead of carrying every activation's code at every store.
+template <int ACT>
+__device__ __forceinline__ float cq_act_t(float v) {
+  if constexpr (ACT == CQ_EPI_ACT_SILU) return v * cq_sigmoid(v);
+  else if constexpr (ACT == CQ_EPI_ACT_GELU_TANH) return v * cq_sigmoid(2.0f * 0.7978845608028654f * (v + 0.044715f * v * v * v));
+  else return 0.5f * v * (1.0f + erff(v * 0.7071067811865476f));
+}
+template <int YT, int ACT>
+__device__ __forceinline__ float cq_epi_apply_t(const CqEpi& e, float v, float b, float u) {
+  v = cq_round_y<YT>(v);
+  if (e.bias) v += b;
+  if constexpr (ACT >= 0) v = cq_act_t<ACT>(v) * u;
+  return v;
+}
 // The one-launch gated product act(g) * u of two fp32 projections, each
 // first rounded to y's dtype.
 template <int YT>

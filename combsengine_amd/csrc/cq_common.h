@@ -6,6 +6,7 @@
 // global_load_dword{,x2,x4} instructions (unaligned access mode is on for
 // amdhsa), never to byte loads.
 #pragma once
+#include <type_traits>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include "cq_epi.h"
@@ -260,4 +261,51 @@ __device__ __forceinline__ void cq_store(void* y, const CqEpi& e, float v, size_
   v = cq_epilogue<YT>(e, v, idx, n);
   if (YT) ((_Float16*)y)[idx] = (_Float16)v;
   else ((float*)y)[idx] = v;
+}
+// Stores a thread's NT x MT MFMA output tiles (row m0 + 16 tm + 4 g + r,
+// column n0 + 16 t + j; value scale[t] * acc[t][tm][r]) through the bias /
+// gated epilogue, for kernels with many outputs per thread.  The activation
+// is chosen once, and every bias and aux value is loaded before the first
+// store: loads and stores share the in-order vmcnt counter, so loads
+// interleaved with stores (or behind a per-value dtype branch, whose join
+// waits) turn the store tail into a chain of memory round trips.  aux must
+// have y's dtype (the gated product's aux is y itself); returns false,
+// storing nothing, when it does not.
+template <int YT, int NT, int MT>
+__device__ __forceinline__ bool cq_store_tiles_epi(const CqEpi& e, void* y, int M, int N, int m0, int n0, int g,
+                                                   int j, const f4 (&acc)[NT][MT], const float (&scale)[NT]) {
+  if (e.aux && e.aux_f16 != YT) return false;
+  auto run = [&](auto actc) {
+    constexpr int ACT = decltype(actc)::value;
+    float bv[NT], uv[NT][MT][4];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      const int nc = min(n0 + 16 * t + j, N - 1);
+      bv[t] = cq_epi_bias(e, nc);
+#pragma unroll
+      for (int tm = 0; tm < MT; tm++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const size_t idx = (size_t)min(m0 + 16 * tm + 4 * g + r, M - 1) * N + nc;
+          uv[t][tm][r] = ACT < 0 ? 0.0f : YT ? (float)((const _Float16*)e.aux)[idx] : ((const float*)e.aux)[idx];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // the loads stay ahead of the stores
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+      for (int tm = 0; tm < MT; tm++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int m = m0 + 16 * tm + 4 * g + r, n = n0 + 16 * t + j;
+          if (m < M && n < N)
+            cq_store_raw<YT>(y, cq_epi_apply_t<YT, ACT>(e, scale[t] * acc[t][tm][r], bv[t], uv[t][tm][r]),
+                             (size_t)m * N + n);
+        }
+  };
+  if (!e.aux) run(std::integral_constant<int, -1>{});
+  else if (e.act == CQ_EPI_ACT_SILU) run(std::integral_constant<int, CQ_EPI_ACT_SILU>{});
+  else if (e.act == CQ_EPI_ACT_GELU_TANH) run(std::integral_constant<int, CQ_EPI_ACT_GELU_TANH>{});
+  else run(std::integral_constant<int, CQ_EPI_ACT_GELU>{});
+  return true;
 }

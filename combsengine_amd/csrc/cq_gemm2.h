@@ -532,56 +532,15 @@ __device__ __forceinline__ void gemm2_body(const LtArgs& a) {
   // path spills a value that its K loop reloads, so it keeps the per-store
   // epilogue below.)
   constexpr bool EPI_T = !(FMT == CQ_Q5_K && NT == 2 && MT == 8);
-  if (EPI_T && !a.part && (a.epi.bias || a.epi.aux) && (!a.epi.aux || a.epi.aux_f16 == YT)) {
-    // Epilogue (bias, gated act(v) * aux): the activation is chosen once for
-    // the workgroup and each variant's store loop is compiled for it alone.
-    // Carrying all three activations (the exact GELU's erff inlined) at each
-    // of a thread's up to 64 unrolled stores made the code ~25k instructions
-    // and the gated gate / up prefill 18944 x 3584 at m = 512 take 159 us
-    // for gate's launch against 119 without the epilogue.  All of a thread's
-    // bias and aux values are loaded before its first store: loads and
-    // stores share the in-order vmcnt counter, so a load issued after a
-    // store waits for it, and loads interleaved with the stores made the
-    // tail a chain of memory round trips.
-    auto store_all = [&](auto actc) {
-      constexpr int ACT = decltype(actc)::value;
-      // every bias and aux value first, then (a scheduling barrier, so the
-      // compiler does not sink the loads back to their uses) every store
-      float bv[NT], uv[NT][MT][4];
-#pragma unroll
-      for (int t = 0; t < NT; t++) {
-        const int nc = min(n0 + 16 * t + s.j, a.N - 1);
-        bv[t] = cq_epi_bias(a.epi, nc);
-#pragma unroll
-        for (int tm = 0; tm < MT; tm++)
-#pragma unroll
-          for (int r = 0; r < 4; r++) {
-            const int m = min(m0 + 16 * tm + 4 * s.g + r, a.M - 1);
-            // aux has y's dtype (checked below): no per-value dtype branch,
-            // whose join would wait for each load before the next
-            const size_t idx = (size_t)m * a.N + nc;
-            uv[t][tm][r] = ACT < 0 ? 0.0f : YT ? (float)((const _Float16*)a.epi.aux)[idx] : ((const float*)a.epi.aux)[idx];
-          }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int t = 0; t < NT; t++)
-#pragma unroll
-        for (int tm = 0; tm < MT; tm++)
-#pragma unroll
-          for (int r = 0; r < 4; r++) {
-            const int m = m0 + 16 * tm + 4 * s.g + r, n = n0 + 16 * t + s.j;
-            if (m < a.M && n < a.N)
-              cq_store_raw<YT>(a.y, cq_epi_apply_t<YT, ACT>(a.epi, s.deff[t] * s.acc[t][tm][r], bv[t], uv[t][tm][r]),
-                               (size_t)m * a.N + n);
-          }
-    };
-    if (!a.epi.aux) store_all(std::integral_constant<int, -1>{});
-    else if (a.epi.act == CQ_EPI_ACT_SILU) store_all(std::integral_constant<int, CQ_EPI_ACT_SILU>{});
-    else if (a.epi.act == CQ_EPI_ACT_GELU_TANH) store_all(std::integral_constant<int, CQ_EPI_ACT_GELU_TANH>{});
-    else store_all(std::integral_constant<int, CQ_EPI_ACT_GELU>{});
+  // Epilogue (bias, gated act(v) * aux): cq_store_tiles_epi picks the
+  // activation once and loads every bias / aux value ahead of the stores.
+  // Carrying all three activations at each of a thread's 64 unrolled stores,
+  // with each aux load waiting for the stores before it, made the gated
+  // gate / up prefill 18944 x 3584 at m = 512 take 159 us for gate's launch
+  // against 119 without the epilogue (now within 1 us of it).
+  if (EPI_T && !a.part && (a.epi.bias || a.epi.aux) &&
+      cq_store_tiles_epi<YT, NT, MT>(a.epi, a.y, a.M, a.N, m0, n0, s.g, s.j, s.acc, s.deff))
     return;
-  }
 #pragma unroll
   for (int t = 0; t < NT; t++) {
 #pragma unroll

@@ -154,6 +154,14 @@ __device__ __forceinline__ void gemml_body(const LgArgs& a) {
     }
     __syncthreads();
   }
+  // bias / gated epilogue: the activation chosen once, the values loaded
+  // ahead of the stores (cq_store_tiles_epi)
+  if (!a.part && (a.epi.bias || a.epi.aux)) {
+    float one[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) one[t] = 1.0f;
+    if (cq_store_tiles_epi<YT, NT, MT>(a.epi, a.y, a.M, a.N, m0, n0, g, j, acc, one)) return;
+  }
 #pragma unroll
   for (int t = 0; t < NT; t++)
 #pragma unroll

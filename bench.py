@@ -490,12 +490,36 @@ def configs_2_3_5(dev):
             tot[mm] += us
         sweep[name] = per
         del pool
+    # gate / up as one cq_matmul_gate_up call, act(gate(h)) * up(h)
+    # (llama.rs:301-303): the layer with that call in place of the two
+    gp, _ = make_pool(QuantFormat.Q4K, 18944, 3584, 0.3 * (1 << 30), seed=5100)
+    upl, _ = make_pool(QuantFormat.Q4K, 18944, 3584, 0.3 * (1 << 30), seed=5101)
+    P = min(len(gp), len(upl))
+    fn = L.lib().cq_matmul_gate_up
+    gated = {}
+    for mm in tot:
+        x = torch.from_numpy(rng.normal(0, 1, (mm, 3584)).astype(np.float16)).to(dev)
+        ytt = torch.float16 if mm > 16 else torch.float32
+        y = torch.empty((mm, 18944), dtype=ytt, device=dev)
+        ydt = L.CQ_F16 if ytt == torch.float16 else L.CQ_F32
+        stream = torch.cuda.current_stream().cuda_stream
+        gh, uh = [w.handle for w in gp], [w.handle for w in upl]
+
+        def launch(i, x=x, y=y, ydt=ydt, mm=mm, stream=stream, gh=gh, uh=uh):
+            st = fn(gh[i % P], uh[i % P], x.data_ptr(), L.CQ_F16, mm, L.CQ_ACT_SILU, y.data_ptr(), ydt, stream)
+            if st != L.CQ_OK:
+                raise RuntimeError(L.last_error())
+        gated[f"m{mm}"], _ = eager_time_us(launch, max(2 * P, 40))
+    del gp, upl
     out["config5_qwen2.5_7b_layer"] = {
-        "weight_bytes": wbytes, "us_per_projection": sweep,
+        "weight_bytes": wbytes, "us_per_projection": sweep, "gate_up_one_call": gated,
         "layer": {f"m{mm}": {"us": round(t, 2), "weight_GBps": round(wbytes / t / 1e3, 1),
                              **({"TFLOPs": round(2.0 * mm * sum(n * k for _, _, n, k in layer) / t / 1e6, 1)}
                                 if mm > 16 else {})}
-                  for mm, t in tot.items()}}
+                  for mm, t in tot.items()},
+        "layer_gate_up_one_call": {
+            f"m{mm}": round(t - sweep["gate"][f"m{mm}"] - sweep["up"][f"m{mm}"] + gated[f"m{mm}"], 2)
+            for mm, t in tot.items()}}
     return out
 
 

@@ -560,8 +560,8 @@ const Knobs& knobs() {
 }
 
 // The no-allocation entry point (cq_matmul_noalloc): while set, the prefill
-// GEMM takes its scratch from this fixed device buffer instead of
-// hipMallocAsync.
+// GEMMs and the batched decode take their scratch from this fixed device
+// buffer instead of the kept (grown on demand) per-device buffers.
 struct FixedScratch {
   void* ptr;
   size_t bytes;

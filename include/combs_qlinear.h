@@ -172,8 +172,9 @@ cq_status cq_quantize(int format, const float* src, int64_t rows, int64_t k, voi
  * for callers that cannot allocate device memory (code under HIP graph
  * capture, serving loops, harnesses that forbid hipMalloc).  Same
  * arguments, kernels and results as cq_matmul; where cq_matmul takes
- * stream-ordered scratch (the prefill GEMM's activation sums and split-K
- * partials, the batched decode's slice partials of long rows) this uses a
+ * scratch from the device's buffers kept across calls (the prefill GEMM's
+ * activation sums and split-K partials, the batched decode's slice partials
+ * of long rows) this uses a
  * fixed 32 MiB device array that the library holds
  * on each device until the process ends, shrinking the K split until the
  * partials fit; a prefill whose activation sums alone (m * K / 8 bytes for

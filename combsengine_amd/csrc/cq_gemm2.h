@@ -8,7 +8,8 @@
 //
 //   - Workgroup tile: 16*MT activation rows x NW waves x NT 16-row weight
 //     tiles (MT = 8: 128 rows, 4 waves, two workgroups per compute unit;
-//     MT = 16: 256 rows, 8 waves, one).  Each wave decodes only its own NT
+//     MT = 16: 256 rows, 8 waves, one; MT = 4: 64 rows, 4 waves, four, for
+//     short prefills).  Each wave decodes only its own NT
 //     weight tiles, straight from packed bytes in registers into exact fp16
 //     MFMA operands (q*sc, as in the decode GEMV), and reuses every decoded
 //     operand for MT MFMAs, one per activation tile.  The packed bytes come

@@ -236,6 +236,7 @@ struct DeviceModule {
   hipFunction_t dequant[kNumFormats] = {};
   hipFunction_t gemm[kNumFormats][2][2] = {};  // K-quant formats only
   hipFunction_t gemm2[kNumFormats][2][2][2] = {};  // [format][NT-1][MT/8-1][y f16], fp16 x
+  hipFunction_t gemm2_m4[kNumFormats][2] = {};      // [format][y f16]: NT = 1, MT = 4
   hipFunction_t xsums = nullptr;
   hipFunction_t reduce[2] = {};       // split-K epilogue [y f16]
   hipFunction_t split_f32 = nullptr;  // fp32 activations -> fp16 hi and lo rows
@@ -331,6 +332,13 @@ void load_module(DeviceModule& d, int dev) {
               return;
             }
           }
+      for (int yt = 0; yt < 2; yt++) {
+        snprintf(name, sizeof name, "cq_gemm2_%s_n1_m4_y%s", fn, yt ? "f16" : "f32");
+        if (get(&d.gemm2_m4[fi][yt], name) != hipSuccess) {
+          d.err = std::string("missing kernel ") + name;
+          return;
+        }
+      }
     }
     snprintf(name, sizeof name, "cq_dequant_%s", fn);
     if (get(&d.dequant[fi], name) != hipSuccess) {
@@ -1244,11 +1252,19 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
     q6_wide = wgs * 5 >= rounds * dm->cus * 4;
   }
   if (q6_wide) mt = 16;
-  if (mt != 8 && mt != 16) mt = 8;
+  // Up to 64 activation rows: MT = 4, four workgroups per compute unit, whose
+  // extra waves hide the per-step load latency that a short prefill cannot
+  // amortise (m = 17 / 64, us: Q4_K 14336 x 4096 28.9 / 32.8 -> 21.7 / 26.7,
+  // Q4_K 18944 x 3584 39.5 / 44.4 -> 25.4 / 36.4, Q6_K 3584 x 18944 45.1 /
+  // 48.5 -> 38.4 / 44.1); from m = 128 the halved reuse of each decoded
+  // operand costs more (Q6_K 4096 x 14336 at m = 128: 54 against 45).
+  if (mt == 0 && m <= 64) mt = 4;
+  if (mt != 4 && mt != 8 && mt != 16) mt = 8;
   // waves per workgroup (the kernels' launch bounds): MT = 16 tiles are one
-  // 8-wave workgroup per compute unit, MT = 8 two 4-wave workgroups
+  // 8-wave workgroup per compute unit, MT = 8 two 4-wave workgroups, MT = 4
+  // four
   const int nw = mt == 16 ? 8 : 4;
-  const long long slots = (long long)dm->cus * (mt == 8 ? 2 : 1);
+  const long long slots = (long long)dm->cus * (mt == 16 ? 1 : mt == 8 ? 2 : 4);
   const long long mblk = (m + 16 * mt - 1) / (16 * mt);
   int nt = knobs().gemm2_nt;
   // NT = 2 while it fills half the slots; Q6_K (long K per superblock pass)
@@ -1256,6 +1272,7 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
   // Q4_K 14336 x 4096 at m = 128 stays faster with one tile, 46.6 against 50.9).
   const long long fill = (w->n + 16 * nw - 1) / (16 * nw) * mblk * 2;
   if (nt != 1 && nt != 2) nt = q6_wide ? 1 : (w->format == CQ_Q6_K ? fill * 4 >= slots * 3 : fill >= slots) ? 2 : 1;
+  if (mt == 4) nt = 1;  // MT = 4 is built with one weight tile per wave
   const long long gx = (w->n + 16 * nw * nt - 1) / (16 * nw * nt);
   if (gx > 0x7fffffffLL || mblk > 65535) return fail(CQ_ERR_BAD_SHAPE, "grid too large");
   // Split K when the tiles leave compute units idle (each slice keeps >= 3
@@ -1279,8 +1296,15 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
   }
   int splits = (cs == hipStreamCaptureStatusNone || fixed) ? knobs().gemm2_split : 1;
   if (splits < 1) {
+    // MT = 4 splits while its grid holds fewer than 1.5 workgroups per
+    // compute unit: filling its four slots per unit measured slower
+    // (14336 x 4096 at m = 17: 21.7 us in two slices, 23.8 in four), one
+    // unsplit 296-workgroup grid too (18944 x 3584: 29.5 against 25.4 in two)
     splits = 1;
-    while (gx * mblk * splits * 2 <= slots && a.units / (splits * 2) >= 3) splits *= 2;
+    if (mt == 4)
+      while (2 * gx * mblk * splits < 3 * (long long)dm->cus && a.units / (splits * 2) >= 3) splits *= 2;
+    else
+      while (gx * mblk * splits * 2 <= slots && a.units / (splits * 2) >= 3) splits *= 2;
   }
   if (splits > a.units) splits = a.units;
   // Scratch: activation sums (Q4_K/Q5_K), then split partials; the device's
@@ -1317,7 +1341,7 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
     }
     if (part_bytes) a.part = (float*)((char*)ws + sums_bytes);
     void* params[] = {&a};
-    hipFunction_t k = dm->gemm2[fi][nt - 1][mt / 8 - 1][yt];
+    hipFunction_t k = mt == 4 ? dm->gemm2_m4[fi][yt] : dm->gemm2[fi][nt - 1][mt / 8 - 1][yt];
     e = klaunch(dm, k, (unsigned)gx, (unsigned)mblk, (unsigned)splits, 64 * nw, 0, s, params);
     if (e != hipSuccess || !part_bytes) return e;
     long long mn = m * w->n;

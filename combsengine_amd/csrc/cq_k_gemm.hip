@@ -31,6 +31,20 @@ GEMM_FMT(q6_k, CQ_Q6_K)
     gemm2_body<FMT, YT, NT, MT, NW>(a);                                                                     \
   }
 #define GEMM2_KERNEL(NAME, FMT, YT, NT, MT) GEMM2_KERNEL_NW(NAME, FMT, YT, NT, MT, (MT == 16 ? 8 : 4))
+// MT = 4 (64 activation rows, one weight tile per wave): 110 registers and
+// 36 KB of LDS, so four 4-wave workgroups share a compute unit (four waves
+// per SIMD) to hide the weight and activation latency of short prefills.
+#define GEMM2_KERNEL_M4(NAME, FMT, YT)                                                             \
+  extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) \
+  NAME(const LtArgs a) {                                                                       \
+    gemm2_body<FMT, YT, 1, 4, 4>(a);                                                           \
+  }
+GEMM2_KERNEL_M4(cq_gemm2_q4_k_n1_m4_yf32, CQ_Q4_K, 0)
+GEMM2_KERNEL_M4(cq_gemm2_q4_k_n1_m4_yf16, CQ_Q4_K, 1)
+GEMM2_KERNEL_M4(cq_gemm2_q5_k_n1_m4_yf32, CQ_Q5_K, 0)
+GEMM2_KERNEL_M4(cq_gemm2_q5_k_n1_m4_yf16, CQ_Q5_K, 1)
+GEMM2_KERNEL_M4(cq_gemm2_q6_k_n1_m4_yf32, CQ_Q6_K, 0)
+GEMM2_KERNEL_M4(cq_gemm2_q6_k_n1_m4_yf16, CQ_Q6_K, 1)
 GEMM2_KERNEL(cq_gemm2_q4_k_n1_m8_yf32, CQ_Q4_K, 0, 1, 8)
 GEMM2_KERNEL(cq_gemm2_q4_k_n1_m8_yf16, CQ_Q4_K, 1, 1, 8)
 GEMM2_KERNEL(cq_gemm2_q4_k_n1_m16_yf32, CQ_Q4_K, 0, 1, 16)

@@ -102,14 +102,13 @@ def test_gemm2_tile_shapes_bit_identical(cuda, monkeypatch, fmt, m):
     x = torch.from_numpy(_x(m, k, 9)).cuda().half()
     monkeypatch.setenv("COMBS_GEMM2_SPLIT", "1")
     outs = {}
-    for nt in ("1", "2"):
-        for mt in ("8", "16"):
-            monkeypatch.setenv("COMBS_GEMM2_NT", nt)
-            monkeypatch.setenv("COMBS_GEMM2_MT", mt)
-            y = torch.empty((m, n), device="cuda")
-            w.matmul_into(x, y, path=L.CQ_PATH_GEMM)
-            torch.cuda.synchronize()
-            outs[(nt, mt)] = _bits(y)
+    for nt, mt in (("1", "4"), ("1", "8"), ("1", "16"), ("2", "8"), ("2", "16")):
+        monkeypatch.setenv("COMBS_GEMM2_NT", nt)
+        monkeypatch.setenv("COMBS_GEMM2_MT", mt)
+        y = torch.empty((m, n), device="cuda")
+        w.matmul_into(x, y, path=L.CQ_PATH_GEMM)
+        torch.cuda.synchronize()
+        outs[(nt, mt)] = _bits(y)
     wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
     O.assert_close(outs[("1", "8")].view(np.float32), x.float().cpu().numpy().astype(np.float64) @ wd.T.astype(
         np.float64), 1e-3, "gemm2")

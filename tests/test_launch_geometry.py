@@ -168,8 +168,12 @@ def splitk_host(units, M, N, cus, mt=8, nt=1, nw=4, fmt="q4_k"):
     mblk = -(-M // (16 * mt))
     gx = -(-N // (16 * nw * nt))
     splits = 1
-    while gx * mblk * splits * 2 <= slots and units // (splits * 2) >= 3:
-        splits *= 2
+    if mt == 4:  # fewer than 1.5 workgroups per compute unit
+        while 2 * gx * mblk * splits < 3 * cus and units // (splits * 2) >= 3:
+            splits *= 2
+    else:
+        while gx * mblk * splits * 2 <= slots and units // (splits * 2) >= 3:
+            splits *= 2
     splits = min(splits, units)
     usplit = -(-units // splits)
     splits = -(-units // usplit)
@@ -178,12 +182,21 @@ def splitk_host(units, M, N, cus, mt=8, nt=1, nw=4, fmt="q4_k"):
     return splits, usplit, sums, part
 
 
+def test_gemm2_short_prefill_splits():
+    # MT = 4 slice counts of the measured shapes (m = 17)
+    assert splitk_host(16, 17, 14336, 256, mt=4)[0] == 2
+    assert splitk_host(14, 17, 18944, 256, mt=4)[0] == 2
+    assert splitk_host(56, 17, 4096, 256, mt=4)[0] == 8
+    assert splitk_host(14, 17, 3584, 256, mt=4)[0] == 4
+
+
 @pytest.mark.parametrize("N,K,M", [(512, 3584, 512), (512, 7168, 64), (3584, 18944, 512), (200, 2560, 130),
+                                   (18944, 3584, 40),
                                    (1024, 4096, 17), (128, 65536, 2048)])
 @pytest.mark.parametrize("fmt", ["q4_k", "q6_k"])
 def test_gemm2_scratch_offsets(N, K, M, fmt):
     units = K // 256
-    splits, usplit, sums, part = splitk_host(units, M, N, 256, fmt=fmt)
+    splits, usplit, sums, part = splitk_host(units, M, N, 256, mt=4 if M <= 64 else 8, fmt=fmt)
     # gemm2_body: slice z covers superblocks [z * usplit, min(+usplit, units))
     covered = []
     for z in range(splits):
@@ -216,9 +229,11 @@ def gemm2_tile_host(fmt, M, N, K, cus=256):
         wgs = t16 * sp
         rounds = -(-wgs // cus)
         wide = wgs * 5 >= rounds * cus * 4
-    mt = 16 if wide else 8
+    mt = 16 if wide else 4 if M <= 64 else 8
     nw = 8 if mt == 16 else 4
-    slots = cus * (2 if mt == 8 else 1)
+    slots = cus * {4: 4, 8: 2, 16: 1}[mt]
+    if mt == 4:
+        return mt, 1, nw
     mblk = -(-M // (16 * mt))
     fill = -(-N // (16 * nw)) * mblk * 2
     if wide:
@@ -243,7 +258,17 @@ def test_gemm2_q6k_tile_choice(N, K, M, wide):
 
 
 @pytest.mark.parametrize("fmt", ["q4_k", "q5_k", "q6_k"])
-@pytest.mark.parametrize("mt,nt,nw", [(8, 1, 4), (8, 2, 4), (16, 1, 8), (16, 2, 8)])
+@pytest.mark.parametrize("M,mt", [(17, 4), (64, 4), (65, 8), (128, 8)])
+def test_gemm2_short_prefill_tile(fmt, M, mt):
+    # MT = 4 (one weight tile per wave) up to 64 activation rows (cq_host.cpp)
+    got_mt, nt, nw = gemm2_tile_host(fmt, M, 14336, 4096)
+    assert (got_mt, nw) == (mt, 4)
+    if mt == 4:
+        assert nt == 1
+
+
+@pytest.mark.parametrize("fmt", ["q4_k", "q5_k", "q6_k"])
+@pytest.mark.parametrize("mt,nt,nw", [(4, 1, 4), (8, 1, 4), (8, 2, 4), (16, 1, 8), (16, 2, 8)])
 @pytest.mark.parametrize("N,K", [(4096, 14336), (128256, 4096), (200, 2560), (3584, 65536)])
 def test_gemm2_dma_cover_and_buffer_offsets(fmt, mt, nt, nw, N, K):
     # gemm2_body: activation DMA instruction i = wave + NW ii moves staged

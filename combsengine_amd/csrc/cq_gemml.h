@@ -5,8 +5,9 @@
 //
 // Work mapping (the prefill GEMM's, cq_gemm2.h, at block granularity):
 //   - workgroup: 4 waves x NT 16-row weight tiles each, x 128 activation rows
-//     (MT = 8 tiles of 16); a step is four 32-value blocks (128 K values);
-//   - the activation chunk of a step (128 rows x 128 halves, 32 KB) arrives
+//     (MT = 8 tiles of 16; 64 rows, MT = 4, for short prefills); a step is
+//     four 32-value blocks (128 K values);
+//   - the activation chunk of a step (16*MT rows x 128 halves, 32 KB at MT = 8) arrives
 //     by global_load_lds one step ahead into the other of two LDS buffers;
 //     16-byte chunk c of row r is stored in slot c ^ (r & 15), so the 16
 //     rows of an A-fragment read hit 16 distinct bank groups;
@@ -43,9 +44,8 @@ constexpr bool lg_affine() {
   return FMT == CQ_Q4_1 || FMT == CQ_Q5_1;
 }
 
-template <int FMT, int YT, int NT, int NW>
+template <int FMT, int YT, int NT, int NW, int MT = 8>
 __device__ __forceinline__ void gemml_body(const LgArgs& a) {
-  constexpr int MT = 8;
   typedef FmtTraits<FMT> T;  // unit = LB = 4 blocks = one step
   typedef typename T::Frag Frag;
   constexpr int BB = T::bytes / LB;  // bytes per block

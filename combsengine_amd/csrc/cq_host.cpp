@@ -251,6 +251,7 @@ struct DeviceModule {
   hipFunction_t gemvq_ms[kNumFormats][3][2] = {};  // Q4_K / Q5_K: min term against the column's sums
   hipFunction_t gemvq_epi[kNumFormats][2][2] = {};  // one weight with the epilogue: [format][_ms][y f16]
   hipFunction_t gemml[kNumFormats][2][2] = {};  // 32-value formats only: [format][NT - 1][y f16]
+  hipFunction_t gemml_m4[kNumFormats][2] = {};   // the same, 64-row tiles (MT = 4), NT = 1
   hipFunction_t gemvr[2][4] = {};  // Q4_K rows split across lanes: [y f16][log2 activation pieces per thread]
   int cus = 0;                        // compute units of the device
   // Scratch kept across calls: [0] batched decode slice partials, [1] the
@@ -404,6 +405,13 @@ void load_module(DeviceModule& d, int dev) {
           return;
         }
       }
+    for (int yt = 0; yt < 2; yt++) {
+      snprintf(name, sizeof name, "cq_gemml_%s_n1_m4_y%s", fmt_name(kFormats[fi]), yt ? "f16" : "f32");
+      if (get(&d.gemml_m4[fi][yt], name) != hipSuccess) {
+        d.err = std::string("missing kernel ") + name;
+        return;
+      }
+    }
   }
   for (int fi = 0; fi < kNumFormats; fi++)
     for (int yt = 0; yt < 2; yt++) {
@@ -516,7 +524,7 @@ constexpr int kUnset = -1000000;
 struct Knobs {
   int gemv_waves, gemv1, gemv1k, gemv1_grid, gemv1_i8, gemv1_prefetch2, gemv1_span, gemv1_spread,
       gemv1_wave_major, gemv2, gemv2_wpc, gemvd, gvd_nt, gvd_waves, gemm_kernel, gemm_waves, gemm2_mt,
-      gemm2_nt, gemm2_split, gateup_fused, gemvr, gemvs, gemvs_split, gemvq, gemvq_groups, gemvq_long, gemvq_msum, f32_split, gemml, gemml_nt, gemml_split,
+      gemm2_nt, gemm2_split, gateup_fused, gemvr, gemvs, gemvs_split, gemvq, gemvq_groups, gemvq_long, gemvq_msum, f32_split, gemml, gemml_mt, gemml_nt, gemml_split,
       multi_fused;
 };
 Knobs g_knobs;
@@ -557,6 +565,7 @@ void read_knobs() {
   k.gemvq_long = env_int("COMBS_GEMVQ_LONG", 1);
   k.f32_split = env_int("COMBS_F32_SPLIT", 1);
   k.gemml = env_int("COMBS_GEMML", 1);
+  k.gemml_mt = env_int("COMBS_GEMML_MT", 0);
   k.gemml_nt = env_int("COMBS_GEMML_NT", 0);
   k.gemml_split = env_int("COMBS_GEMML_SPLIT", 0);
   k.multi_fused = env_int("COMBS_MULTI_FUSED", 1);
@@ -1387,9 +1396,14 @@ static cq_status launch_gemml(DeviceModule* dm, const cq_weight* w, const void* 
   a.K = (int)w->k;
   a.blocks = (int)(w->k / 32);
   a.epi = epi;
-  const long long mblk = (m + 127) / 128;
+  // MT = 4 (64 activation rows, four workgroups per compute unit) up to
+  // m = 64, as for the K-quant prefill; else MT = 8 (128 rows, two per unit)
+  int mt = knobs().gemml_mt;
+  if (mt != 4 && mt != 8) mt = m <= 64 ? 4 : 8;
+  const long long mblk = (m + 16 * mt - 1) / (16 * mt);
   int nt = knobs().gemml_nt;
   if (nt != 1 && nt != 2) nt = ((w->n + 127) / 128) * mblk >= dm->cus ? 2 : 1;
+  if (mt == 4) nt = 1;
   const long long gx = (w->n + 64 * nt - 1) / (64 * nt);
   if (gx > 0x7fffffffLL || mblk > 65535) return fail(CQ_ERR_BAD_SHAPE, "grid too large");
   // K slices while the grid leaves compute units idle (two workgroups fit
@@ -1408,7 +1422,10 @@ static cq_status launch_gemml(DeviceModule* dm, const cq_weight* w, const void* 
   int splits = (cs == hipStreamCaptureStatusNone || fixed) ? knobs().gemml_split : 1;
   if (splits < 1) {
     splits = 1;
-    while (gx * mblk * splits * 2 <= 2LL * dm->cus && steps / (splits * 2) >= 3) splits *= 2;
+    if (mt == 4)  // to 1.5 workgroups per compute unit, as for the K-quant prefill
+      while (2 * gx * mblk * splits < 3LL * dm->cus && steps / (splits * 2) >= 3) splits *= 2;
+    else
+      while (gx * mblk * splits * 2 <= 2LL * dm->cus && steps / (splits * 2) >= 3) splits *= 2;
   }
   if (splits > steps) splits = steps;
   auto part_size = [&](int sp) -> size_t { return sp > 1 ? (size_t)sp * m * w->n * 4 : 0; };
@@ -1420,7 +1437,7 @@ static cq_status launch_gemml(DeviceModule* dm, const cq_weight* w, const void* 
   auto launch_all = [&](void* ws) -> hipError_t {
     if (part_bytes) a.part = (float*)ws;
     void* params[] = {&a};
-    hipError_t e = klaunch(dm, dm->gemml[fi][nt - 1][yt], (unsigned)gx, (unsigned)mblk, (unsigned)splits, 256, 0, s,
+    hipError_t e = klaunch(dm, mt == 4 ? dm->gemml_m4[fi][yt] : dm->gemml[fi][nt - 1][yt], (unsigned)gx, (unsigned)mblk, (unsigned)splits, 256, 0, s,
                            params);
     if (e == hipSuccess && part_bytes) {
       long long mn = m * w->n;

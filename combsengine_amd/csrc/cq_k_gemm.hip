@@ -109,6 +109,21 @@ extern "C" __global__ void __launch_bounds__(256) cq_split_f32(const float* x, _
   GEMML_KERNEL(cq_gemml_##fname##_n1_yf16, FMT, 1, 1)  \
   GEMML_KERNEL(cq_gemml_##fname##_n2_yf32, FMT, 0, 2)  \
   GEMML_KERNEL(cq_gemml_##fname##_n2_yf16, FMT, 1, 2)
+// 64 activation rows (MT = 4), one weight tile per wave: four workgroups per
+// compute unit for short prefills
+#define GEMML_KERNEL_M4(NAME, FMT, YT)                                                             \
+  extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) \
+  NAME(const LgArgs a) {                                                                       \
+    gemml_body<FMT, YT, 1, 4, 4>(a);                                                           \
+  }
+#define GEMML_FMT_M4(fname, FMT)                          \
+  GEMML_KERNEL_M4(cq_gemml_##fname##_n1_m4_yf32, FMT, 0) \
+  GEMML_KERNEL_M4(cq_gemml_##fname##_n1_m4_yf16, FMT, 1)
+GEMML_FMT_M4(q4_0, CQ_Q4_0)
+GEMML_FMT_M4(q5_0, CQ_Q5_0)
+GEMML_FMT_M4(q8_0, CQ_Q8_0)
+GEMML_FMT_M4(q4_1, CQ_Q4_1)
+GEMML_FMT_M4(q5_1, CQ_Q5_1)
 GEMML_FMT(q4_0, CQ_Q4_0)
 GEMML_FMT(q5_0, CQ_Q5_0)
 GEMML_FMT(q8_0, CQ_Q8_0)

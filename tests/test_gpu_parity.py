@@ -714,18 +714,19 @@ def test_gemv_batched_shared(cuda, monkeypatch, fmt, split, n, k, m):
 
 
 @pytest.mark.parametrize("fmt", sorted(LEGACY))
-@pytest.mark.parametrize("nt", ["1", "2"])
+@pytest.mark.parametrize("mt,nt", [("8", "1"), ("8", "2"), ("4", "1")])
 @pytest.mark.parametrize("split", ["0", "1", "3"])
 @pytest.mark.parametrize("n,k,m", [(300, 320, 17), (130, 4096, 64), (1000, 1056, 130), (70, 2048, 300)])
-def test_gemm_legacy_formats(cuda, monkeypatch, fmt, nt, split, n, k, m):
-    """Prefill GEMM for the 32-value formats (cq_gemml_*): 128-row activation
-    tiles (ragged m), 16-row weight tiles (ragged n), steps of four blocks
+def test_gemm_legacy_formats(cuda, monkeypatch, fmt, mt, nt, split, n, k, m):
+    """Prefill GEMM for the 32-value formats (cq_gemml_*): 128- or 64-row
+    activation tiles (ragged m), 16-row weight tiles (ragged n), steps of four blocks
     with a partial last step (k = 320, 1056), one or two weight tiles per
     wave, the steps split over the grid (automatic, one, three slices: the
     last shorter, or holding only the partial step) with the slices'
     partials summed by cq_splitk_reduce_*; fp32 and fp16 y and the bias
     epilogue, against the oracle."""
     import torch
+    monkeypatch.setenv("COMBS_GEMML_MT", mt)
     monkeypatch.setenv("COMBS_GEMML_NT", nt)
     monkeypatch.setenv("COMBS_GEMML_SPLIT", split)
     data = synth(fmt, n, k)
@@ -735,8 +736,8 @@ def test_gemm_legacy_formats(cuda, monkeypatch, fmt, nt, split, n, k, m):
     expect = O.ref_matmul(x, wd)
     xd = torch.from_numpy(x).cuda().half()
     kern = L.path_name(w, xd, torch.empty((m, n), device="cuda"))
-    print(f"gemml {fmt.name} nt={nt} n={n} k={k} m={m} kernels={kern}", flush=True)
-    assert kern.startswith(f"cq_gemml_{fmt.name.lower()}_n{nt}")
+    print(f"gemml {fmt.name} mt={mt} nt={nt} n={n} k={k} m={m} kernels={kern}", flush=True)
+    assert kern.startswith(f"cq_gemml_{fmt.name.lower()}_n{nt}" + ("_m4" if mt == "4" else "_y"))
     O.assert_close(_run(w, x, torch.float16, torch.float32), expect, 1e-3, "y32")
     O.assert_close(_run(w, x, torch.float16, torch.float16), expect, 1e-3, "y16")
     b = np.linspace(-2, 2, n).astype(np.float32)

@@ -116,6 +116,31 @@ def test_gemm2_tile_shapes_bit_identical(cuda, monkeypatch, fmt, m):
         assert np.array_equal(v, outs[("1", "8")]), f"tile {key} differs from (1, 8)"
 
 
+@pytest.mark.parametrize("fmt", [F.Q4_0, F.Q5_0, F.Q8_0, F.Q4_1, F.Q5_1])
+@pytest.mark.parametrize("m", [17, 64, 130])
+def test_gemml_tile_shapes_bit_identical(cuda, monkeypatch, fmt, m):
+    """Legacy-format prefill: 64- and 128-row activation tiles and one or two
+    weight tiles per wave give the same bits (the K split held fixed)."""
+    import torch
+    n, k = 520, 2048
+    data, w = _weight(fmt, n, k, 910 + int(fmt))
+    x = torch.from_numpy(_x(m, k, 12)).cuda().half()
+    monkeypatch.setenv("COMBS_GEMML_SPLIT", "2")
+    outs = {}
+    for mt, nt in (("4", "1"), ("8", "1"), ("8", "2")):
+        monkeypatch.setenv("COMBS_GEMML_MT", mt)
+        monkeypatch.setenv("COMBS_GEMML_NT", nt)
+        y = torch.empty((m, n), device="cuda")
+        w.matmul_into(x, y)
+        torch.cuda.synchronize()
+        outs[(mt, nt)] = _bits(y)
+    wd = O.dequant(int(fmt), data, n * k).reshape(n, k)
+    O.assert_close(outs[("8", "1")].view(np.float32), x.float().cpu().numpy().astype(np.float64) @ wd.T.astype(
+        np.float64), 1e-3, "gemml")
+    for key, v in outs.items():
+        assert np.array_equal(v, outs[("8", "1")]), f"tile {key} differs from (8, 1)"
+
+
 @pytest.mark.parametrize("fmt", KQ)
 @pytest.mark.parametrize("nw", ["2", "4"])
 def test_gemvd_row_tiles_bit_identical(cuda, monkeypatch, fmt, nw):

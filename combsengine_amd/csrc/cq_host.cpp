@@ -1266,8 +1266,13 @@ static cq_status launch_gemm2(DeviceModule* dm, const cq_weight* w, const void* 
   // amortise (m = 17 / 64, us: Q4_K 14336 x 4096 28.9 / 32.8 -> 21.7 / 26.7,
   // Q4_K 18944 x 3584 39.5 / 44.4 -> 25.4 / 36.4, Q6_K 3584 x 18944 45.1 /
   // 48.5 -> 38.4 / 44.1); from m = 128 the halved reuse of each decoded
-  // operand costs more (Q6_K 4096 x 14336 at m = 128: 54 against 45).
-  if (mt == 0 && m <= 64) mt = 4;
+  // operand costs more (Q6_K 4096 x 14336 at m = 128: 54 against 45), except
+  // for Q4_K weights whose 64-row tiles fill the compute units unsplit up to
+  // m = 128 (14336 x 4096: 36.7 against 39.7 us; 18944 x 3584: 49.9 against
+  // 53.4; 4096 x 14336 stays on MT = 8: 38.8 against 37.8).
+  if (mt == 0 && (m <= 64 || (w->format == CQ_Q4_K && m <= 128 &&
+                              (w->n + 63) / 64 * ((m + 63) / 64) >= dm->cus)))
+    mt = 4;
   if (mt != 4 && mt != 8 && mt != 16) mt = 8;
   // waves per workgroup (the kernels' launch bounds): MT = 16 tiles are one
   // 8-wave workgroup per compute unit, MT = 8 two 4-wave workgroups, MT = 4

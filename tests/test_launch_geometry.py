@@ -229,7 +229,7 @@ def gemm2_tile_host(fmt, M, N, K, cus=256):
         wgs = t16 * sp
         rounds = -(-wgs // cus)
         wide = wgs * 5 >= rounds * cus * 4
-    mt = 16 if wide else 4 if M <= 64 else 8
+    mt = 16 if wide else 4 if M <= 64 or (fmt == "q4_k" and M <= 128 and -(-N // 64) * -(-M // 64) >= cus) else 8
     nw = 8 if mt == 16 else 4
     slots = cus * {4: 4, 8: 2, 16: 1}[mt]
     if mt == 4:
@@ -258,9 +258,13 @@ def test_gemm2_q6k_tile_choice(N, K, M, wide):
 
 
 @pytest.mark.parametrize("fmt", ["q4_k", "q5_k", "q6_k"])
-@pytest.mark.parametrize("M,mt", [(17, 4), (64, 4), (65, 8), (128, 8)])
+@pytest.mark.parametrize("M,mt", [(17, 4), (64, 4), (65, 8), (128, 8), (129, 8)])
 def test_gemm2_short_prefill_tile(fmt, M, mt):
-    # MT = 4 (one weight tile per wave) up to 64 activation rows (cq_host.cpp)
+    # MT = 4 (one weight tile per wave) up to 64 activation rows, for Q4_K
+    # weights that fill the compute units up to 128 (cq_host.cpp)
+    if fmt == "q4_k" and 64 < M <= 128:
+        mt = 4
+    assert gemm2_tile_host(fmt, M, 4096, 14336)[0] == (4 if M <= 64 else 8)
     got_mt, nt, nw = gemm2_tile_host(fmt, M, 14336, 4096)
     assert (got_mt, nw) == (mt, 4)
     if mt == 4:
